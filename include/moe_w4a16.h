@@ -1,0 +1,165 @@
+/*
+ * moe_w4a16.h - C ABI of the MI355X (gfx950) GPTQ-int4 W4A16 fused-MoE library
+ * (libmoe_w4a16.so, built from mtp_amd/csrc/).
+ *
+ * Conventions (mirroring the reference's native ABI style,
+ * microbench/premap_kernel_consumer/premap_payload_cache_inprocess_native_producer_stub.hip:505-595
+ * and its ctypes binding in src/mtp_expert_prefetch/tracing/vllm_router_trace.py:8383-8445):
+ *   - every entry point is `extern "C" int name_v1(...)`, returning 0 on success,
+ *     1xx for argument/shape errors and 2xx for HIP runtime errors; the message of
+ *     the last failure on the calling thread is returned by moe_w4a16_last_error();
+ *   - every tensor pointer is a DEVICE pointer owned by the caller;
+ *   - `stream` is a hipStream_t (NULL = the null stream); calls are stream-ordered,
+ *     never synchronise the host and never allocate device memory;
+ *   - bf16 and fp16 values travel as uint16_t bit patterns.
+ *
+ * Tensor layouts are the reference's repacked GPTQ layout
+ * (src/mtp_expert_prefetch/repack/qwen3_moe_gptq.py:142-198, store.py:126-137),
+ * stacked over experts:
+ *   qweight int32 [E, K/8, N]   nibble j of qweight[e, r, n] is W[e, 8r + j, n]
+ *   qzeros  int32 [E, K/G, N/8] nibble j of qzeros[e, g, c]  is Z[e, g, 8c + j]
+ *   scales  fp16  [E, K/G, N]
+ *   dequantised W[k, n] = (W_int - Z[g(k), n]) * S[g(k), n],  g(k) = k / G
+ *   (src/mtp_expert_prefetch/repack/gptq_unpack.py:54-131).
+ */
+#ifndef MOE_W4A16_H
+#define MOE_W4A16_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_W4A16_ABI_VERSION 1
+
+enum {
+  MOE_OK = 0,
+  MOE_ERR_NULL = 101,        /* a required pointer is NULL */
+  MOE_ERR_SHAPE = 102,       /* a size is out of the supported range or inconsistent */
+  MOE_ERR_UNSUPPORTED = 103, /* a valid but unsupported configuration */
+  MOE_ERR_WORKSPACE = 104,   /* workspace too small */
+  MOE_ERR_HIP = 200          /* 200 + (hipError_t % 100): HIP runtime error */
+};
+
+/* One GPTQ projection stacked over experts (or over the slots of a pool). */
+typedef struct moe_gptq_proj_v1 {
+  const int32_t* qweight;
+  const int32_t* qzeros;
+  const uint16_t* scales;
+} moe_gptq_proj_v1;
+
+/* A set of int4 experts of one layer: gate/up [E, H/8, I], down [E, I/8, H].
+ * expert_row: NULL, or a device int32 [num_experts] map from expert id to the row
+ * of the stacked tensors that holds it (an HBM slot pool). */
+typedef struct moe_expert_set_v1 {
+  moe_gptq_proj_v1 gate;
+  moe_gptq_proj_v1 up;
+  moe_gptq_proj_v1 down;
+  const int32_t* expert_row;
+  int32_t num_experts;
+  int32_t hidden;
+  int32_t intermediate;
+  int32_t group_size;
+} moe_expert_set_v1;
+
+/* Kernel path selection for the expert GEMMs. */
+enum { MOE_PATH_AUTO = 0, MOE_PATH_DECODE = 1, MOE_PATH_PREFILL = 2 };
+
+int moe_w4a16_abi_version(void);
+const char* moe_w4a16_last_error(void);
+
+/* Dequantise num_experts stacked projections to bf16.
+ * Replaces dequantize_gptq_projection (src/mtp_expert_prefetch/repack/gptq_unpack.py:88-131).
+ * g_idx: NULL (g = k / group_size) or device int32 [num_experts, in_features]; out-of-range
+ * entries are clamped (the host wrapper rejects them first, as the reference does at :119-124).
+ * out_dtype: 0 bf16, 1 fp16, 2 fp32. out: [E, out, in] when linear_weight != 0, else [E, in, out].
+ * Bit-exact with the reference for every output dtype (the fp32 product is exact). */
+int moe_dequant_v1(const moe_gptq_proj_v1* proj, const int32_t* g_idx, int32_t num_experts,
+                   int32_t in_features, int32_t out_features, int32_t group_size,
+                   int32_t linear_weight, int32_t out_dtype, void* out, void* stream);
+
+/* Router: logits = x . router_w^T (+ logit_bias) in fp32, softmax, top-k, renormalise.
+ * Replaces the gate GEMV (src/mtp_expert_prefetch/mtp/extra_tensors.py:353) and vLLM
+ * topk_softmax(renormalize=True) as restated at
+ * src/mtp_expert_prefetch/tracing/vllm_router_trace.py:4201-4225.
+ * Ties: larger logit first, equal logits -> lower expert id.
+ * x bf16 [T, H]; router_w bf16 [E, H]; logit_bias NULL or fp32 [E]; shared_gate_w NULL or
+ * bf16 [H]. logits: fp32 workspace [T, E + 1]. topk_ids int32 [T, top_k];
+ * topk_weights fp32 [T * top_k (+ T when shared_gate_w != NULL)]: entry T*top_k + t holds
+ * sigmoid(x[t] . shared_gate_w) (extra_tensors.py:596). */
+int moe_router_topk_v1(const uint16_t* x, int32_t T, int32_t hidden, const uint16_t* router_w,
+                       int32_t num_experts, const float* logit_bias, int32_t top_k,
+                       const uint16_t* shared_gate_w, float* logits, int32_t* topk_ids,
+                       float* topk_weights, void* stream);
+
+/* Number of block_m blocks the aligned layout may need (grid size of the GEMMs). */
+int moe_capacity_blocks_v1(int32_t T, int32_t top_k, int32_t num_experts, int32_t has_shared,
+                           int32_t block_m);
+
+/* Token->expert align/sort: flat slots f = t*top_k + i (plus T shared slots T*top_k + t
+ * routed to expert id num_experts when has_shared) grouped by expert (ascending), slots
+ * ascending inside a group, each group padded to block_m with the sentinel
+ * num_slots = T*top_k (+T). Replaces vLLM moe_align_block_size
+ * (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19647-19660; format pinned by
+ * tests/test_vllm_descriptor_mapping_assertion.py:1012-1085).
+ * sorted_ids int32 [capacity_blocks*block_m]; expert_ids int32 [capacity_blocks] (-1 for
+ * unused blocks); ntpp int32 [1]. Slots whose id is outside [0, E) are dropped. */
+int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_experts,
+                 int32_t has_shared, int32_t block_m, int32_t capacity_blocks,
+                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, void* stream);
+
+/* W1: h[f, :] = silu(x[tok(f)] . Wgate[e]^T) * (x[tok(f)] . Wup[e]^T) for every slot f of
+ * every block (bf16 h [num_slots, I]). Replaces invoke_fused_moe_wna16_triton_kernel for
+ * W1 + silu_and_mul (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19674-19718,
+ * arithmetic at src/mtp_expert_prefetch/tracing/vllm_wna16_group_plan.py:367-486).
+ * shared: NULL or the shared expert (expert id num_experts). */
+int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
+                          const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                          const int32_t* sorted_ids, const int32_t* expert_ids,
+                          const int32_t* ntpp, int32_t block_m, int32_t capacity_blocks,
+                          uint16_t* h, int32_t path, void* stream);
+
+/* W2: ys[f, :] = topk_weights[f] * (h[f] . Wdown[e]^T), fp32 [num_slots, H].
+ * Replaces the W2 dispatch with mul_routed_weight=True, top_k=1
+ * (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19761-19783). */
+int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
+                   const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                   const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                   int32_t block_m, int32_t capacity_blocks, const float* topk_weights,
+                   float* ys, int32_t path, void* stream);
+
+/* out[t, :] = bf16(sum_{i<top_k} ys[t*top_k + i, :] (+ ys[T*top_k + t, :])), fixed order.
+ * Replaces ops.moe_sum (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19801-19804). */
+int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
+               uint16_t* out, void* stream);
+
+/* Workspace bytes for moe_layer_v1 / moe_fused_experts_v1. */
+int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_set_v1* experts,
+                                     int32_t has_shared, int32_t path);
+
+/* Full routed layer: router -> align -> W1 -> W2 -> sum (+ sigmoid-gated shared expert).
+ * Replaces fused_experts_impl (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19330-19817)
+ * with its router (:17934, :21719) and MtpExtraRunner.moe_tokens
+ * (src/mtp_expert_prefetch/mtp/extra_tensors.py:544-598). out bf16 [T, H].
+ * topk_ids_out / topk_weights_out: NULL or int32 [T, top_k] / fp32 [T, top_k] copies. */
+int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const float* logit_bias,
+                 int32_t top_k, const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                 const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                 uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
+                 void* stream);
+
+/* Experts with caller-given routing: topk_ids int32 [T, top_k], topk_weights fp32 [T, top_k].
+ * Replaces TopKExpertMlp.forward (src/mtp_expert_prefetch/repack/gptq_unpack.py:293-327)
+ * and moe_tokens with given ids (src/mtp_expert_prefetch/mtp/extra_tensors.py:544-598). */
+int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
+                         const float* topk_weights, int32_t top_k,
+                         const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                         const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                         uint16_t* out, int32_t path, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_W4A16_H */

@@ -1,0 +1,131 @@
+"""ctypes binding of libmoe_w4a16.so (the C ABI declared in include/moe_w4a16.h).
+
+Mirrors the reference's native-library binding style: ``ctypes.CDLL`` with explicit
+argtypes/restype, integer return codes turned into Python exceptions
+(src/mtp_expert_prefetch/tracing/vllm_router_trace.py:8383-8445).
+
+There is no fallback: if the library is missing the import of an op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+LIB_NAME = "libmoe_w4a16.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+ABI_VERSION = 1
+
+MOE_OK = 0
+MOE_ERR_NULL = 101
+MOE_ERR_SHAPE = 102
+MOE_ERR_UNSUPPORTED = 103
+MOE_ERR_WORKSPACE = 104
+MOE_ERR_HIP = 200
+
+PATH_AUTO = 0
+PATH_DECODE = 1
+PATH_PREFILL = 2
+
+EXPORTED = (
+    "moe_w4a16_abi_version",
+    "moe_w4a16_last_error",
+    "moe_dequant_v1",
+    "moe_router_topk_v1",
+    "moe_capacity_blocks_v1",
+    "moe_align_v1",
+    "moe_w1_gateup_silu_v1",
+    "moe_w2_down_v1",
+    "moe_sum_v1",
+    "moe_layer_workspace_bytes_v1",
+    "moe_layer_v1",
+    "moe_fused_experts_v1",
+)
+
+
+class GptqProj(ctypes.Structure):
+    _fields_ = [("qweight", c_void_p), ("qzeros", c_void_p), ("scales", c_void_p)]
+
+
+class ExpertSet(ctypes.Structure):
+    _fields_ = [
+        ("gate", GptqProj),
+        ("up", GptqProj),
+        ("down", GptqProj),
+        ("expert_row", c_void_p),
+        ("num_experts", c_int32),
+        ("hidden", c_int32),
+        ("intermediate", c_int32),
+        ("group_size", c_int32),
+    ]
+
+
+class MoeLibraryError(RuntimeError):
+    def __init__(self, code: int, message: str) -> None:
+        super().__init__(f"[moe_w4a16 error {code}] {message}")
+        self.code = code
+
+
+_LIB: ctypes.CDLL | None = None
+
+_P = c_void_p
+_I = c_int32
+_SIGS = {
+    "moe_w4a16_abi_version": ([], c_int32),
+    "moe_w4a16_last_error": ([], c_char_p),
+    "moe_dequant_v1": ([POINTER(GptqProj), _P, _I, _I, _I, _I, _I, _I, _P, _P], c_int32),
+    "moe_router_topk_v1": ([_P, _I, _I, _P, _I, _P, _I, _P, _P, _P, _P, _P], c_int32),
+    "moe_capacity_blocks_v1": ([_I, _I, _I, _I, _I], c_int32),
+    "moe_align_v1": ([_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P], c_int32),
+    "moe_w1_gateup_silu_v1": (
+        [_P, _I, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, _P, _I, _I, _P, _I, _P],
+        c_int32),
+    "moe_w2_down_v1": (
+        [_P, _I, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, _P, _I, _I, _P, _P, _I, _P],
+        c_int32),
+    "moe_sum_v1": ([_P, _I, _I, _I, _I, _P, _P], c_int32),
+    "moe_layer_workspace_bytes_v1": ([_I, _I, POINTER(ExpertSet), _I, _I], c_int64),
+    "moe_layer_v1": (
+        [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _P, _P,
+         _I, _P],
+        c_int32),
+    "moe_fused_experts_v1": (
+        [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _I, _P],
+        c_int32),
+}
+
+
+def lib_path() -> Path:
+    override = os.environ.get("MTP_AMD_LIB")
+    return Path(override) if override else LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once; raise if it is missing or its ABI does not match."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = lib_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is missing: the MI355X kernels are not built. "
+            "Run `python -m mtp_amd.build` (or __graft_entry__.build()) first; there is no CPU fallback."
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (argtypes, restype) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    version = lib.moe_w4a16_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {version}, expected {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def check(code: int) -> None:
+    if code != MOE_OK:
+        msg = load().moe_w4a16_last_error().decode("utf-8", "replace")
+        raise MoeLibraryError(code, msg)

@@ -1,0 +1,361 @@
+// extern "C" entry points of libmoe_w4a16.so: argument validation, workspace carving and
+// stream-ordered orchestration of the kernels. No entry point allocates device memory or
+// synchronises the host.
+#include <cstdarg>
+#include <cstdio>
+
+#include "common.h"
+#include "launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(MOE_ERR_HIP + ((int)e % 100), "%s: HIP error %d (%s)", where, (int)e,
+              hipGetErrorString(e));
+}
+
+#define MOE_CHECK_HIP(expr, where)                 \
+  do {                                             \
+    hipError_t _e = (expr);                        \
+    if (_e != hipSuccess) return hip_fail(_e, where); \
+  } while (0)
+
+bool proj_ok(const moe_gptq_proj_v1& p) { return p.qweight && p.qzeros && p.scales; }
+
+ProjDev to_dev(const moe_gptq_proj_v1& p) { return ProjDev{p.qweight, p.qzeros, p.scales}; }
+
+// Shapes every GEMM kernel supports (checked once per call).
+int check_experts(const moe_expert_set_v1* ex, const moe_expert_set_v1* sh) {
+  if (!ex) return fail(MOE_ERR_NULL, "experts is NULL");
+  if (!proj_ok(ex->gate) || !proj_ok(ex->up) || !proj_ok(ex->down))
+    return fail(MOE_ERR_NULL, "an expert projection pointer is NULL");
+  const int H = ex->hidden, I = ex->intermediate, G = ex->group_size;
+  if (ex->num_experts < 1 || ex->num_experts > 512)
+    return fail(MOE_ERR_SHAPE, "num_experts=%d outside [1, 512]", ex->num_experts);
+  if (H < 512 || H > 2048 || H % 512 != 0)
+    return fail(MOE_ERR_SHAPE, "hidden=%d must be a multiple of 512 in [512, 2048]", H);
+  if (!(I == 256 || I == 512 || I == 1024))
+    return fail(MOE_ERR_SHAPE, "intermediate=%d must be one of 256, 512, 1024", I);
+  if (G < 64 || G % 64 != 0 || H % G != 0 || I % G != 0)
+    return fail(MOE_ERR_SHAPE, "group_size=%d unsupported for hidden=%d intermediate=%d", G, H,
+                I);
+  if (sh) {
+    if (!proj_ok(sh->gate) || !proj_ok(sh->up) || !proj_ok(sh->down))
+      return fail(MOE_ERR_NULL, "a shared-expert projection pointer is NULL");
+    if (sh->num_experts != 1 || sh->hidden != H || sh->intermediate != I || sh->group_size != G)
+      return fail(MOE_ERR_SHAPE, "shared expert must be one expert of the routed experts' shape");
+  }
+  return MOE_OK;
+}
+
+ExpertsDev make_experts_dev(const moe_expert_set_v1* ex, const moe_expert_set_v1* sh) {
+  ExpertsDev d{};
+  d.gate = to_dev(ex->gate);
+  d.up = to_dev(ex->up);
+  d.down = to_dev(ex->down);
+  if (sh) {
+    d.sgate = to_dev(sh->gate);
+    d.sup = to_dev(sh->up);
+    d.sdown = to_dev(sh->down);
+  }
+  d.expert_row = ex->expert_row;
+  d.num_experts = ex->num_experts;
+  d.hidden = ex->hidden;
+  d.inter = ex->intermediate;
+  d.group = ex->group_size;
+  return d;
+}
+
+int resolve_path(int path, int T, int top_k) {
+  if (path == MOE_PATH_DECODE || path == MOE_PATH_PREFILL) return path;
+  return (T * top_k >= 1024) ? MOE_PATH_PREFILL : MOE_PATH_DECODE;
+}
+
+int block_m_of(int path) { return path == MOE_PATH_PREFILL ? kPrefillBlockM : kDecodeBlockM; }
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct Workspace {
+  size_t logits, ids, w, sorted, eids, ntpp, h, ys, total;
+  int cap, bm;
+};
+
+Workspace layout(int T, int top_k, const moe_expert_set_v1* ex, int has_shared, int path) {
+  Workspace L{};
+  const int E = ex->num_experts, H = ex->hidden, I = ex->intermediate;
+  const size_t slots = (size_t)T * top_k + (has_shared ? T : 0);
+  L.bm = block_m_of(path);
+  L.cap = align_capacity_blocks(T, top_k, E, has_shared, L.bm);
+  size_t o = 0;
+  L.logits = o; o += align256((size_t)T * (E + 1) * 4);
+  L.ids = o;    o += align256((size_t)T * top_k * 4);
+  L.w = o;      o += align256(slots * 4);
+  L.sorted = o; o += align256((size_t)L.cap * L.bm * 4);
+  L.eids = o;   o += align256((size_t)L.cap * 4);
+  L.ntpp = o;   o += 256;
+  L.h = o;      o += align256(slots * I * 2);
+  L.ys = o;     o += align256(slots * H * 4);
+  L.total = o;
+  return L;
+}
+
+template <typename T>
+T* at(void* base, size_t off) { return reinterpret_cast<T*>(static_cast<char*>(base) + off); }
+
+// align -> W1 -> W2 -> sum over a routed workspace (ids and weights already in place).
+int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex,
+                const moe_expert_set_v1* sh, const Workspace& L, void* ws, uint16_t* out,
+                int path, hipStream_t stream) {
+  const int has_shared = sh ? 1 : 0;
+  const ExpertsDev ed = make_experts_dev(ex, sh);
+  SlotsDev sd{T, top_k, T * top_k + (has_shared ? T : 0)};
+  int32_t* ids = at<int32_t>(ws, L.ids);
+  float* w = at<float>(ws, L.w);
+  int32_t* sorted = at<int32_t>(ws, L.sorted);
+  int32_t* eids = at<int32_t>(ws, L.eids);
+  int32_t* ntpp = at<int32_t>(ws, L.ntpp);
+  uint16_t* h = at<uint16_t>(ws, L.h);
+  float* ys = at<float>(ws, L.ys);
+  MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted, eids,
+                             ntpp, stream), "align");
+  if (path == MOE_PATH_PREFILL) {
+    MOE_CHECK_HIP(launch_w1_prefill(x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream),
+                  "w1 prefill");
+    MOE_CHECK_HIP(launch_w2_prefill(h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
+                  "w2 prefill");
+  } else {
+    MOE_CHECK_HIP(launch_w1_decode(x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream),
+                  "w1 decode");
+    MOE_CHECK_HIP(launch_w2_decode(h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
+                  "w2 decode");
+  }
+  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, out, stream), "moe_sum");
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_w4a16_abi_version(void) { return MOE_W4A16_ABI_VERSION; }
+
+const char* moe_w4a16_last_error(void) { return g_err; }
+
+int moe_dequant_v1(const moe_gptq_proj_v1* proj, const int32_t* g_idx, int32_t num_experts,
+                   int32_t in_features, int32_t out_features, int32_t group_size,
+                   int32_t linear_weight, int32_t out_dtype, void* out, void* stream) {
+  if (!proj || !proj_ok(*proj) || !out) return fail(MOE_ERR_NULL, "dequant: NULL pointer");
+  if (out_dtype < 0 || out_dtype > 2)
+    return fail(MOE_ERR_UNSUPPORTED, "dequant: out_dtype=%d (0 bf16, 1 fp16, 2 fp32)", out_dtype);
+  if (num_experts < 1 || num_experts > 65535)
+    return fail(MOE_ERR_SHAPE, "dequant: num_experts=%d", num_experts);
+  if (in_features <= 0 || in_features % 8 != 0 || out_features <= 0 || out_features % 8 != 0)
+    return fail(MOE_ERR_SHAPE, "dequant: in=%d out=%d must be positive multiples of 8",
+                in_features, out_features);
+  if (in_features / 8 > 65535) return fail(MOE_ERR_SHAPE, "dequant: in_features too large");
+  if (group_size <= 0 || in_features % group_size != 0)
+    return fail(MOE_ERR_SHAPE, "dequant: group_size=%d does not divide in_features=%d",
+                group_size, in_features);
+  MOE_CHECK_HIP(launch_dequant(to_dev(*proj), g_idx, num_experts, in_features, out_features,
+                               group_size, linear_weight, out_dtype, out, (hipStream_t)stream),
+                "dequant");
+  return MOE_OK;
+}
+
+int moe_router_topk_v1(const uint16_t* x, int32_t T, int32_t hidden, const uint16_t* router_w,
+                       int32_t num_experts, const float* logit_bias, int32_t top_k,
+                       const uint16_t* shared_gate_w, float* logits, int32_t* topk_ids,
+                       float* topk_weights, void* stream) {
+  if (T < 0) return fail(MOE_ERR_SHAPE, "router: T=%d", T);
+  if (T == 0) return MOE_OK;
+  if (!x || !router_w || !logits || !topk_ids || !topk_weights)
+    return fail(MOE_ERR_NULL, "router: NULL pointer");
+  if (hidden <= 0 || hidden % 8 != 0) return fail(MOE_ERR_SHAPE, "router: hidden=%d", hidden);
+  if (num_experts < 1 || num_experts > 512)
+    return fail(MOE_ERR_SHAPE, "router: num_experts=%d outside [1, 512]", num_experts);
+  if (top_k < 1 || top_k > num_experts || top_k > 64)
+    return fail(MOE_ERR_SHAPE, "router: top_k=%d outside [1, min(num_experts, 64)]", top_k);
+  hipStream_t s = (hipStream_t)stream;
+  MOE_CHECK_HIP(launch_router_logits(x, T, hidden, router_w, num_experts, shared_gate_w,
+                                     logit_bias, logits, s), "router logits");
+  MOE_CHECK_HIP(launch_router_topk(logits, T, num_experts, top_k, shared_gate_w ? 1 : 0, topk_ids,
+                                   topk_weights, s), "router topk");
+  return MOE_OK;
+}
+
+int moe_capacity_blocks_v1(int32_t T, int32_t top_k, int32_t num_experts, int32_t has_shared,
+                           int32_t block_m) {
+  if (T < 0 || top_k < 1 || num_experts < 1 || block_m < 1) return 0;
+  return align_capacity_blocks(T, top_k, num_experts, has_shared ? 1 : 0, block_m);
+}
+
+int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_experts,
+                 int32_t has_shared, int32_t block_m, int32_t capacity_blocks,
+                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, void* stream) {
+  if (!sorted_ids || !expert_ids || !ntpp || (T > 0 && !topk_ids))
+    return fail(MOE_ERR_NULL, "align: NULL pointer");
+  if (T < 0 || top_k < 1 || top_k > 64) return fail(MOE_ERR_SHAPE, "align: T=%d top_k=%d", T, top_k);
+  if (num_experts < 1 || num_experts > 512)
+    return fail(MOE_ERR_SHAPE, "align: num_experts=%d outside [1, 512]", num_experts);
+  if (block_m < 1 || block_m > 1024) return fail(MOE_ERR_SHAPE, "align: block_m=%d", block_m);
+  if ((int64_t)T * (top_k + 1) > (1 << 22)) return fail(MOE_ERR_SHAPE, "align: too many slots");
+  const int need = align_capacity_blocks(T, top_k, num_experts, has_shared ? 1 : 0, block_m);
+  if (capacity_blocks < need)
+    return fail(MOE_ERR_WORKSPACE, "align: capacity_blocks=%d < required %d", capacity_blocks,
+                need);
+  MOE_CHECK_HIP(launch_align(topk_ids, T, top_k, num_experts, has_shared ? 1 : 0, block_m,
+                             capacity_blocks, sorted_ids, expert_ids, ntpp, (hipStream_t)stream),
+                "align");
+  return MOE_OK;
+}
+
+int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
+                          const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                          const int32_t* sorted_ids, const int32_t* expert_ids,
+                          const int32_t* ntpp, int32_t block_m, int32_t capacity_blocks,
+                          uint16_t* h, int32_t path, void* stream) {
+  int rc = check_experts(experts, shared);
+  if (rc) return rc;
+  if (T < 0 || top_k < 1) return fail(MOE_ERR_SHAPE, "w1: T=%d top_k=%d", T, top_k);
+  if (T == 0) return MOE_OK;
+  if (!x || !sorted_ids || !expert_ids || !ntpp || !h) return fail(MOE_ERR_NULL, "w1: NULL pointer");
+  path = resolve_path(path, T, top_k);
+  if (block_m != block_m_of(path))
+    return fail(MOE_ERR_UNSUPPORTED, "w1: block_m=%d, path %d needs %d", block_m, path,
+                block_m_of(path));
+  const ExpertsDev ed = make_experts_dev(experts, shared);
+  const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
+  hipStream_t s = (hipStream_t)stream;
+  if (path == MOE_PATH_PREFILL)
+    MOE_CHECK_HIP(launch_w1_prefill(x, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+                                    capacity_blocks, h, s), "w1 prefill");
+  else
+    MOE_CHECK_HIP(launch_w1_decode(x, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+                                   capacity_blocks, h, s), "w1 decode");
+  return MOE_OK;
+}
+
+int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
+                   const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                   const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
+                   int32_t block_m, int32_t capacity_blocks, const float* topk_weights,
+                   float* ys, int32_t path, void* stream) {
+  int rc = check_experts(experts, shared);
+  if (rc) return rc;
+  if (T < 0 || top_k < 1) return fail(MOE_ERR_SHAPE, "w2: T=%d top_k=%d", T, top_k);
+  if (T == 0) return MOE_OK;
+  if (!h || !sorted_ids || !expert_ids || !ntpp || !topk_weights || !ys)
+    return fail(MOE_ERR_NULL, "w2: NULL pointer");
+  path = resolve_path(path, T, top_k);
+  if (block_m != block_m_of(path))
+    return fail(MOE_ERR_UNSUPPORTED, "w2: block_m=%d, path %d needs %d", block_m, path,
+                block_m_of(path));
+  const ExpertsDev ed = make_experts_dev(experts, shared);
+  const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
+  hipStream_t s = (hipStream_t)stream;
+  if (path == MOE_PATH_PREFILL)
+    MOE_CHECK_HIP(launch_w2_prefill(h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+                                    capacity_blocks, topk_weights, ys, s), "w2 prefill");
+  else
+    MOE_CHECK_HIP(launch_w2_decode(h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+                                   capacity_blocks, topk_weights, ys, s), "w2 decode");
+  return MOE_OK;
+}
+
+int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
+               uint16_t* out, void* stream) {
+  if (T < 0 || top_k < 1 || hidden <= 0 || hidden % 4 != 0)
+    return fail(MOE_ERR_SHAPE, "moe_sum: T=%d top_k=%d hidden=%d", T, top_k, hidden);
+  if (T == 0) return MOE_OK;
+  if (!ys || !out) return fail(MOE_ERR_NULL, "moe_sum: NULL pointer");
+  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, hidden, has_shared ? 1 : 0, out, (hipStream_t)stream),
+                "moe_sum");
+  return MOE_OK;
+}
+
+int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_set_v1* experts,
+                                     int32_t has_shared, int32_t path) {
+  if (!experts || T < 0 || top_k < 1) return -1;
+  path = resolve_path(path, T, top_k);
+  return (int64_t)layout(T, top_k, experts, has_shared ? 1 : 0, path).total;
+}
+
+int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const float* logit_bias,
+                 int32_t top_k, const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                 const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                 uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
+                 void* stream) {
+  int rc = check_experts(experts, shared);
+  if (rc) return rc;
+  if (T < 0) return fail(MOE_ERR_SHAPE, "layer: T=%d", T);
+  if (T == 0) return MOE_OK;
+  if (!x || !router_w || !out || !workspace) return fail(MOE_ERR_NULL, "layer: NULL pointer");
+  if (shared && !shared_gate_w) return fail(MOE_ERR_NULL, "layer: shared expert needs shared_gate_w");
+  const int E = experts->num_experts;
+  if (top_k < 1 || top_k > E || top_k > 64)
+    return fail(MOE_ERR_SHAPE, "layer: top_k=%d outside [1, min(num_experts, 64)]", top_k);
+  path = resolve_path(path, T, top_k);
+  const Workspace L = layout(T, top_k, experts, shared ? 1 : 0, path);
+  if (workspace_bytes < (int64_t)L.total)
+    return fail(MOE_ERR_WORKSPACE, "layer: workspace %lld < required %lld",
+                (long long)workspace_bytes, (long long)L.total);
+  hipStream_t s = (hipStream_t)stream;
+  float* logits = at<float>(workspace, L.logits);
+  int32_t* ids = at<int32_t>(workspace, L.ids);
+  float* w = at<float>(workspace, L.w);
+  MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E,
+                                     shared ? shared_gate_w : nullptr, logit_bias, logits, s),
+                "router logits");
+  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, shared ? 1 : 0, ids, w, s), "router topk");
+  rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, s);
+  if (rc) return rc;
+  if (topk_ids_out)
+    MOE_CHECK_HIP(hipMemcpyAsync(topk_ids_out, ids, (size_t)T * top_k * 4,
+                                 hipMemcpyDeviceToDevice, s), "copy ids");
+  if (topk_weights_out)
+    MOE_CHECK_HIP(hipMemcpyAsync(topk_weights_out, w, (size_t)T * top_k * 4,
+                                 hipMemcpyDeviceToDevice, s), "copy weights");
+  return MOE_OK;
+}
+
+int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
+                         const float* topk_weights, int32_t top_k,
+                         const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                         const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                         uint16_t* out, int32_t path, void* stream) {
+  int rc = check_experts(experts, shared);
+  if (rc) return rc;
+  if (T < 0 || top_k < 1 || top_k > 64) return fail(MOE_ERR_SHAPE, "experts: T=%d top_k=%d", T, top_k);
+  if (T == 0) return MOE_OK;
+  if (!x || !topk_ids || !topk_weights || !out || !workspace)
+    return fail(MOE_ERR_NULL, "experts: NULL pointer");
+  if (shared && !shared_gate_w) return fail(MOE_ERR_NULL, "experts: shared expert needs shared_gate_w");
+  path = resolve_path(path, T, top_k);
+  const Workspace L = layout(T, top_k, experts, shared ? 1 : 0, path);
+  if (workspace_bytes < (int64_t)L.total)
+    return fail(MOE_ERR_WORKSPACE, "experts: workspace %lld < required %lld",
+                (long long)workspace_bytes, (long long)L.total);
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* ids = at<int32_t>(workspace, L.ids);
+  float* w = at<float>(workspace, L.w);
+  MOE_CHECK_HIP(hipMemcpyAsync(ids, topk_ids, (size_t)T * top_k * 4, hipMemcpyDeviceToDevice, s),
+                "copy ids");
+  MOE_CHECK_HIP(hipMemcpyAsync(w, topk_weights, (size_t)T * top_k * 4, hipMemcpyDeviceToDevice, s),
+                "copy weights");
+  if (shared)
+    MOE_CHECK_HIP(launch_shared_gate(x, T, experts->hidden, shared_gate_w, top_k,
+                                     at<float>(workspace, L.logits), w, s), "shared gate");
+  return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,98 @@
+// Shared device helpers for the gfx950 W4A16 MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_w4a16.h"
+
+#define MOE_DEV __device__ __forceinline__
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 "magic" exponent: a bf16 with bit pattern 0x4300 | q (q < 16) has value 128 + q.
+constexpr uint32_t kMagicPair = 0x43004300u;
+constexpr float kMagicBias = 128.0f;
+
+MOE_DEV float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+MOE_DEV float bf16lo_to_f32(uint32_t pair) { return __uint_as_float(pair << 16); }
+MOE_DEV float bf16hi_to_f32(uint32_t pair) { return __uint_as_float(pair & 0xFFFF0000u); }
+
+// fp32 -> bf16, IEEE round-to-nearest-even (NaN kept quiet).
+MOE_DEV uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+MOE_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+}
+
+MOE_DEV float f16_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// D = a.lo*b.lo + a.hi*b.hi + c  (v_dot2_f32_bf16)
+MOE_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Pairs (x[j], x[j+4]) of the 8 bf16 held in d0..d3 (d0 = x0|x1<<16, ...), matching the
+// nibble pairs (j, j+4) produced by magic_pair().
+MOE_DEV void xpairs(const u32x4 d, uint32_t p[4]) {
+  p[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);  // (x0, x4)
+  p[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);  // (x1, x5)
+  p[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);  // (x2, x6)
+  p[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);  // (x3, x7)
+}
+
+// bf16 pair (128 + nibble j, 128 + nibble j+4) of a packed int32 of 8 nibbles.
+MOE_DEV uint32_t magic_pair(uint32_t w, int j) {
+  return ((w >> (4 * j)) & 0x000F000Fu) | kMagicPair;
+}
+
+MOE_DEV u32x4 ld128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+MOE_DEV u32x4 ld128_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+MOE_DEV float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+// Device view of one projection of an expert set.
+struct ProjDev {
+  const int32_t* qweight;
+  const int32_t* qzeros;
+  const uint16_t* scales;
+};
+
+// Everything a GEMM kernel needs to locate expert e's weights.
+struct ExpertsDev {
+  ProjDev gate, up, down;
+  ProjDev sgate, sup, sdown;     // shared expert (expert id == num_experts), may be null
+  const int32_t* expert_row;     // nullable
+  int32_t num_experts;
+  int32_t hidden, inter, group;
+};
+
+MOE_DEV int64_t expert_row(const ExpertsDev& ed, int e) {
+  return ed.expert_row ? (int64_t)ed.expert_row[e] : (int64_t)e;
+}
+
+// Per-call sizes shared by the kernels.
+struct SlotsDev {
+  int32_t T;          // tokens
+  int32_t top_k;
+  int32_t num_slots;  // T*top_k (+T with a shared expert)
+};
+
+MOE_DEV int slot_token(const SlotsDev& s, int f) {
+  return f < s.T * s.top_k ? f / s.top_k : f - s.T * s.top_k;
+}
+
+MOE_DEV float wave_xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }

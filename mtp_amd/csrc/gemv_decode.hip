@@ -1,0 +1,271 @@
+// Decode path: grouped int4 GEMV for W1 (gate_up + SiLU*mul) and W2 (down * routed weight),
+// and the fixed-order top-k sum. HBM-bound: every packed int32 of an expert's weights is
+// read once per block with 128-bit coalesced loads and dequantised in registers.
+//
+// Arithmetic (src/mtp_expert_prefetch/tracing/vllm_wna16_group_plan.py:367-486 and
+// src/mtp_expert_prefetch/repack/gptq_unpack.py:88-131, 247-256):
+//   y[n] = sum_k x[k] * (q[k,n] - z[g,n]) * s[g,n]
+// is evaluated per lane over a k-range inside one quantisation group g as
+//   s[g,n] * ( sum_k x[k]*(128 + q[k,n])  -  (128 + z[g,n]) * sum_k x[k] ),
+// where (128 + q) is built as an exact bf16 by OR-ing the nibble into the mantissa of 128.0
+// (one v_and_or per two weights) and the sums run on v_dot2_f32_bf16. All products are exact;
+// the result differs from the reference's bf16-rounded dequantised weight only by that
+// reference rounding (<= 2^-9 relative per weight).
+//
+// Thread layout of a block (one expert block of BM slots x one 32-column tile):
+//   cq = tid & 7       -> columns c .. c+3 (one 128-bit load of 4 packed int32)
+//   ks = tid >> 3      -> packed rows ks*RPK .. ks*RPK+RPK-1 (8*RPK consecutive k, inside one group)
+// so blockDim = K / RPK. A wave load instruction reads 8 rows x 128 contiguous bytes. Partials
+// over ks are reduced with xor-shuffles (lane bits 3..5) and then across waves through LDS,
+// always in the same order, so results are deterministic.
+#include "common.h"
+#include "launch.h"
+
+namespace {
+
+constexpr uint32_t kOnePair = 0x3F803F80u;  // bf16 (1.0, 1.0)
+constexpr int kRPK = 4;                     // packed rows (8*kRPK k) per lane
+constexpr int kMaxWaves = 8;                // K <= 2048 -> blockDim <= 512
+
+enum { GEMV_W1 = 1, GEMV_W2 = 2 };
+
+MOE_DEV int block_valid_run(const int32_t* __restrict__ sorted, int base, int m, int BM,
+                            int num_slots, int maxn) {
+  int n = 0;
+  for (int j = 0; j < maxn && m + j < BM; ++j) {
+    if (sorted[base + m + j] >= num_slots) break;
+    ++n;
+  }
+  return n;
+}
+
+// Weights, scales and zeros of one lane: NP projections (W1: gate, up; W2: down).
+template <int NP>
+struct LaneTile {
+  u32x4 w[NP][kRPK];
+  float s[NP][4], z[NP][4];
+};
+
+template <int MODE, int NT>
+MOE_DEV void gemv_tokens(const uint16_t* __restrict__ act, int K, int NOUT, const int (&f)[NT],
+                         const int (&arow)[NT], const LaneTile<(MODE == GEMV_W1 ? 2 : 1)>& lt,
+                         int tid, int nwaves, int col0, float (*red)[8][8][1],
+                         const float* __restrict__ topk_w, uint16_t* __restrict__ h,
+                         float* __restrict__ ys) {
+  constexpr int NP = (MODE == GEMV_W1) ? 2 : 1;
+  const int lane = tid & 63, wave = tid >> 6, cq = tid & 7, ks = tid >> 3;
+  float acc[NT][NP][4], xs[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    xs[j] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[j][p][q] = 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < kRPK; ++r) {
+    const int k0 = (ks * kRPK + r) * 8;
+    uint32_t xp[NT][4];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const u32x4 d = ld128(act + (int64_t)arow[j] * K + k0);
+      xpairs(d, xp[j]);
+      xs[j] = dot2_bf16(xp[j][0], kOnePair, xs[j]);
+      xs[j] = dot2_bf16(xp[j][1], kOnePair, xs[j]);
+      xs[j] = dot2_bf16(xp[j][2], kOnePair, xs[j]);
+      xs[j] = dot2_bf16(xp[j][3], kOnePair, xs[j]);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t wq = lt.w[p][r][q];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          const uint32_t mq = magic_pair(wq, pr);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[j][p][q] = dot2_bf16(mq, xp[j][pr], acc[j][p][q]);
+        }
+      }
+  }
+  // lane partial: s * (sum x*(128+q) - (128+z) * sum x), then reduce over ks inside the wave
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float t = lt.s[p][q] * (acc[j][p][q] - lt.z[p][q] * xs[j]);
+        t = wave_xor_sum(t, 8);
+        t = wave_xor_sum(t, 16);
+        t = wave_xor_sum(t, 32);
+        acc[j][p][q] = t;
+      }
+  if ((lane >> 3) == 0) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[wave * 4 + j][cq][p * 4 + q][0] = acc[j][p][q];
+  }
+  __syncthreads();
+  if (tid < NT * 8) {
+    const int j = tid >> 3, q8 = tid & 7;
+    float v[NP][4];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[p][q] = 0.0f;
+    for (int w = 0; w < nwaves; ++w)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[p][q] += red[w * 4 + j][q8][p * 4 + q][0];
+    int fj = f[0];
+#pragma unroll
+    for (int jj = 1; jj < NT; ++jj)
+      if (j == jj) fj = f[jj];
+    const int c = col0 + q8 * 4;
+    if (MODE == GEMV_W1) {
+      u32x2 o;
+      o[0] = pack_bf16x2(silu_f32(v[0][0]) * v[NP - 1][0], silu_f32(v[0][1]) * v[NP - 1][1]);
+      o[1] = pack_bf16x2(silu_f32(v[0][2]) * v[NP - 1][2], silu_f32(v[0][3]) * v[NP - 1][3]);
+      *reinterpret_cast<u32x2*>(h + (int64_t)fj * NOUT + c) = o;
+    } else {
+      const float w = topk_w[fj];
+      f32x4 o = {v[0][0] * w, v[0][1] * w, v[0][2] * w, v[0][3] * w};
+      *reinterpret_cast<f32x4*>(ys + (int64_t)fj * NOUT + c) = o;
+    }
+  }
+  __syncthreads();
+}
+
+// W1 (MODE_W1): act = x [T, H], K = H, NOUT = I, out h bf16 [slots, I] = silu(gate) * up.
+// W2 (MODE_W2): act = h [slots, I], K = I, NOUT = H, out ys fp32 [slots, H] = w * down.
+template <int MODE>
+__global__ __launch_bounds__(512) void gemv_decode_kernel(const uint16_t* __restrict__ act,
+                                                          ExpertsDev ed, SlotsDev sd,
+                                                          const int32_t* __restrict__ sorted,
+                                                          const int32_t* __restrict__ eids,
+                                                          const int32_t* __restrict__ ntpp,
+                                                          int BM, const float* __restrict__ topk_w,
+                                                          uint16_t* __restrict__ h,
+                                                          float* __restrict__ ys) {
+  constexpr int NP = (MODE == GEMV_W1) ? 2 : 1;
+  // red[wave*4 + token][cq][value][0]; the trailing dimension keeps the declared shape simple.
+  __shared__ float red[kMaxWaves * 4][8][8][1];
+  const int b = blockIdx.y;
+  if (b * BM >= *ntpp) return;
+  const int e = eids[b];
+  if (e < 0) return;
+  const int G = ed.group;
+  const int K = (MODE == GEMV_W1) ? ed.hidden : ed.inter;
+  const int NOUT = (MODE == GEMV_W1) ? ed.inter : ed.hidden;
+  const int tid = threadIdx.x, ks = tid >> 3, cq = tid & 7;
+  const int nwaves = blockDim.x >> 6;
+  const int col0 = blockIdx.x * 32;
+  const int c = col0 + cq * 4;
+  const bool is_shared = (e == ed.num_experts);
+  ProjDev pj[NP];
+  if (MODE == GEMV_W1) {
+    pj[0] = is_shared ? ed.sgate : ed.gate;
+    pj[NP - 1] = is_shared ? ed.sup : ed.up;
+  } else {
+    pj[0] = is_shared ? ed.sdown : ed.down;
+  }
+  const int64_t row = is_shared ? 0 : expert_row(ed, e);
+  const int K8 = K / 8, NG = K / G;
+  const int g = (ks * kRPK * 8) / G;
+
+  LaneTile<NP> lt;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int32_t* wq = pj[p].qweight + (row * K8 + ks * kRPK) * NOUT + c;
+#pragma unroll
+    for (int r = 0; r < kRPK; ++r) lt.w[p][r] = ld128_nt(wq + (int64_t)r * NOUT);
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const u32x2 s2 = *reinterpret_cast<const u32x2*>(pj[p].scales + (row * NG + g) * NOUT + c);
+    const uint32_t zw = (uint32_t)pj[p].qzeros[(row * NG + g) * (NOUT / 8) + (c >> 3)];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      lt.s[p][q] = f16_to_f32((s2[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+      lt.z[p][q] = kMagicBias + (float)((zw >> (4 * ((c & 7) + q))) & 0xFu);
+    }
+  }
+  const int base = b * BM;
+  int m = 0;
+  while (m < BM) {
+    const int n = block_valid_run(sorted, base, m, BM, sd.num_slots, 2);
+    if (n == 0) break;
+    if (n == 2) {
+      int f[2], ar[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f[j] = sorted[base + m + j];
+        ar[j] = (MODE == GEMV_W1) ? slot_token(sd, f[j]) : f[j];
+      }
+      gemv_tokens<MODE, 2>(act, K, NOUT, f, ar, lt, tid, nwaves, col0, red, topk_w, h, ys);
+      m += 2;
+    } else {
+      int f[1], ar[1];
+      f[0] = sorted[base + m];
+      ar[0] = (MODE == GEMV_W1) ? slot_token(sd, f[0]) : f[0];
+      gemv_tokens<MODE, 1>(act, K, NOUT, f, ar, lt, tid, nwaves, col0, red, topk_w, h, ys);
+      m += 1;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------- moe_sum
+__global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ ys, int T,
+                                                      int top_k, int H, int has_shared,
+                                                      uint16_t* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = H / 4;
+  const int64_t t = idx / per_row;
+  if (t >= T) return;
+  const int c = (int)(idx % per_row) * 4;
+  f32x4 s = *reinterpret_cast<const f32x4*>(ys + (t * top_k) * H + c);
+  for (int i = 1; i < top_k; ++i) s += *reinterpret_cast<const f32x4*>(ys + (t * top_k + i) * H + c);
+  if (has_shared) s += *reinterpret_cast<const f32x4*>(ys + ((int64_t)T * top_k + t) * H + c);
+  u32x2 o;
+  o[0] = pack_bf16x2(s[0], s[1]);
+  o[1] = pack_bf16x2(s[2], s[3]);
+  *reinterpret_cast<u32x2*>(out + t * H + c) = o;
+}
+
+}  // namespace
+
+hipError_t launch_w1_decode(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                            const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                            int BM, int cap, uint16_t* h, hipStream_t stream) {
+  // blockDim = 8 column-quads x H / (8 kRPK) k-subsets; one 32-column tile per block.
+  const dim3 grid(ed.inter / 32, cap);
+  const dim3 block(ed.hidden / kRPK);
+  hipLaunchKernelGGL(gemv_decode_kernel<GEMV_W1>, grid, block, 0, stream, x, ed, sd, sorted, eids,
+                     ntpp, BM, (const float*)nullptr, h, (float*)nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                            const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                            int BM, int cap, const float* topk_w, float* ys, hipStream_t stream) {
+  const dim3 grid(ed.hidden / 32, cap);
+  const dim3 block(ed.inter / kRPK);
+  hipLaunchKernelGGL(gemv_decode_kernel<GEMV_W2>, grid, block, 0, stream, h, ed, sd, sorted, eids,
+                     ntpp, BM, topk_w, (uint16_t*)nullptr, ys);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared, uint16_t* out,
+                          hipStream_t stream) {
+  const int64_t n = (int64_t)T * (H / 4);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(moe_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ys,
+                     T, top_k, H, has_shared, out);
+  return hipGetLastError();
+}

@@ -1,0 +1,47 @@
+// Host-side launchers of the kernels (one translation unit per kernel family).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct ProjDev;
+struct ExpertsDev;
+struct SlotsDev;
+
+hipError_t launch_dequant(const ProjDev& p, const int32_t* g_idx, int E, int K, int N, int G,
+                          int linear, int out_dtype, void* out, hipStream_t stream);
+
+hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t* W, int E,
+                                const uint16_t* shared_w, const float* bias, float* logits,
+                                hipStream_t stream);
+hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
+                              int32_t* ids, float* weights, hipStream_t stream);
+hipError_t launch_shared_gate(const uint16_t* x, int T, int H, const uint16_t* shared_w,
+                              int top_k, float* logits_ws, float* weights, hipStream_t stream);
+
+int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM);
+hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
+                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp,
+                        hipStream_t stream);
+
+// Decode (VALU GEMV) path.
+hipError_t launch_w1_decode(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                            const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                            int BM, int cap, uint16_t* h, hipStream_t stream);
+hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                            const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                            int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
+hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared, uint16_t* out,
+                          hipStream_t stream);
+
+// Prefill (bf16 MFMA) path.
+hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                             const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                             int BM, int cap, uint16_t* h, hipStream_t stream);
+hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                             const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                             int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
+
+// Block sizes (slots per block) of the two paths.
+constexpr int kDecodeBlockM = 16;
+constexpr int kPrefillBlockM = 128;

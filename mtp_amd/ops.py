@@ -1,0 +1,268 @@
+"""Tensor-level wrappers of the C ABI. Every op runs the HIP kernels; none has a CPU path.
+
+All tensors must live on one ROCm device; outputs are allocated with torch (caching
+allocator, so the ops are safe to capture in a HIP graph) and every launch goes to
+torch.cuda.current_stream().
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from mtp_amd import _lib
+from mtp_amd.weights import MoeExperts
+
+PATHS = {"auto": _lib.PATH_AUTO, "decode": _lib.PATH_DECODE, "prefill": _lib.PATH_PREFILL}
+DECODE_BLOCK_M = 16
+PREFILL_BLOCK_M = 128
+OUT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> None:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("the W4A16 MoE kernels need ROCm device tensors; got a CPU tensor")
+        if not t.is_contiguous():
+            raise ValueError("tensors passed to the W4A16 MoE kernels must be contiguous")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+
+
+def _path(path: str | int) -> int:
+    if isinstance(path, int):
+        return path
+    try:
+        return PATHS[path]
+    except KeyError as exc:
+        raise ValueError(f"path must be one of {sorted(PATHS)}") from exc
+
+
+def _bf16_matrix(x: torch.Tensor, name: str, cols: int | None = None) -> None:
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {x.dtype}")
+    if x.ndim != 2:
+        raise ValueError(f"{name} must be 2D, got {tuple(x.shape)}")
+    if cols is not None and x.shape[1] != cols:
+        raise ValueError(f"Expected {name} last dim {cols}, got {x.shape[1]}")
+
+
+# ----------------------------------------------------------------------------- dequant
+def dequantize(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+               g_idx: torch.Tensor | None = None, *, group_size: int = 128,
+               linear_weight: bool = True, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """HIP dequant of one ([K/8, N]) or stacked ([E, K/8, N]) GPTQ projection.
+
+    Bit-exact with dequantize_gptq_projection
+    (src/mtp_expert_prefetch/repack/gptq_unpack.py:88-131)."""
+    lib = _lib.load()
+    squeeze = qweight.ndim == 2
+    if squeeze:
+        qweight, qzeros, scales = qweight[None], qzeros[None], scales[None]
+        if g_idx is not None:
+            g_idx = g_idx[None]
+    _require_gpu(qweight, qzeros, scales, g_idx)
+    if dtype not in OUT_DTYPES:
+        raise ValueError(f"Unsupported dtype {dtype}")
+    e, k8, n = qweight.shape
+    k = k8 * 8
+    out_shape = (e, n, k) if linear_weight else (e, k, n)
+    out = torch.empty(out_shape, dtype=dtype, device=qweight.device)
+    proj = _lib.GptqProj(qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr())
+    gi = None
+    if g_idx is not None:
+        gi = g_idx.to(torch.int32).contiguous()
+    _lib.check(lib.moe_dequant_v1(ctypes.byref(proj), _ptr(gi), e, k, n, group_size,
+                                  1 if linear_weight else 0, OUT_DTYPES[dtype], out.data_ptr(),
+                                  _stream()))
+    return out[0] if squeeze else out
+
+
+# ----------------------------------------------------------------------------- router
+def router_topk(x: torch.Tensor, router_w: torch.Tensor, top_k: int = 8, *,
+                logit_bias: torch.Tensor | None = None,
+                shared_gate_w: torch.Tensor | None = None):
+    """fp32 logits -> softmax -> top-k -> renormalise (bit-exact ids, ties to the lower id).
+
+    Returns (topk_ids int32 [T, k], topk_weights fp32 [T, k], shared_gate fp32 [T] or None,
+    logits fp32 [T, E])."""
+    lib = _lib.load()
+    _bf16_matrix(x, "input")
+    _bf16_matrix(router_w, "router_w", x.shape[1])
+    _require_gpu(x, router_w, logit_bias, shared_gate_w)
+    T, E = x.shape[0], router_w.shape[0]
+    if not 0 < top_k <= E:
+        raise ValueError(f"top_k must be in [1, {E}], got {top_k}")
+    dev = x.device
+    logits = torch.empty(T, E + 1, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    has_shared = shared_gate_w is not None
+    w = torch.empty(T * top_k + (T if has_shared else 0), dtype=torch.float32, device=dev)
+    if logit_bias is not None and (logit_bias.dtype != torch.float32 or logit_bias.numel() != E):
+        raise ValueError("logit_bias must be float32 [E]")
+    if has_shared:
+        if shared_gate_w.dtype != torch.bfloat16 or shared_gate_w.numel() != x.shape[1]:
+            raise ValueError("shared_gate_w must be bfloat16 with hidden elements")
+    _lib.check(lib.moe_router_topk_v1(x.data_ptr(), T, x.shape[1], router_w.data_ptr(), E,
+                                      _ptr(logit_bias), top_k, _ptr(shared_gate_w),
+                                      logits.data_ptr(), ids.data_ptr(), w.data_ptr(), _stream()))
+    topk_w = w[: T * top_k].view(T, top_k)
+    shared = w[T * top_k:] if has_shared else None
+    return ids, topk_w, shared, logits[:, :E]
+
+
+# ----------------------------------------------------------------------------- align
+def capacity_blocks(T: int, top_k: int, num_experts: int, has_shared: bool, block_m: int) -> int:
+    return int(_lib.load().moe_capacity_blocks_v1(T, top_k, num_experts, int(has_shared), block_m))
+
+
+def align(topk_ids: torch.Tensor, num_experts: int, block_m: int, *, has_shared: bool = False,
+          capacity: int | None = None):
+    """Block-padded expert-grouped slot permutation (vLLM moe_align_block_size format)."""
+    lib = _lib.load()
+    if topk_ids.dtype != torch.int32 or topk_ids.ndim != 2:
+        raise TypeError("topk_ids must be int32 [T, k]")
+    _require_gpu(topk_ids)
+    T, k = topk_ids.shape
+    cap = capacity if capacity is not None else capacity_blocks(T, k, num_experts, has_shared, block_m)
+    dev = topk_ids.device
+    sorted_ids = torch.empty(cap * block_m, dtype=torch.int32, device=dev)
+    eids = torch.empty(cap, dtype=torch.int32, device=dev)
+    ntpp = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.check(lib.moe_align_v1(topk_ids.data_ptr(), T, k, num_experts, int(has_shared), block_m,
+                                cap, sorted_ids.data_ptr(), eids.data_ptr(), ntpp.data_ptr(),
+                                _stream()))
+    return sorted_ids, eids, ntpp
+
+
+# ----------------------------------------------------------------------------- GEMMs
+def _block_m(path: int, T: int, top_k: int) -> int:
+    if path == _lib.PATH_AUTO:
+        path = _lib.PATH_PREFILL if T * top_k >= 1024 else _lib.PATH_DECODE
+    return PREFILL_BLOCK_M if path == _lib.PATH_PREFILL else DECODE_BLOCK_M
+
+
+def w1_gateup_silu(x, experts: MoeExperts, sorted_ids, expert_ids, ntpp, *, top_k: int,
+                   shared: MoeExperts | None = None, path: str | int = "auto") -> torch.Tensor:
+    lib = _lib.load()
+    p = _path(path)
+    T = x.shape[0]
+    bm = _block_m(p, T, top_k)
+    slots = T * top_k + (T if shared is not None else 0)
+    h = torch.empty(slots, experts.intermediate_size, dtype=torch.bfloat16, device=x.device)
+    ex = experts.struct()
+    sh = shared.struct() if shared is not None else None
+    _lib.check(lib.moe_w1_gateup_silu_v1(
+        x.data_ptr(), T, top_k, ctypes.byref(ex), ctypes.byref(sh) if sh else None,
+        sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(), bm, expert_ids.numel(),
+        h.data_ptr(), p, _stream()))
+    return h
+
+
+def w2_down(h, experts: MoeExperts, sorted_ids, expert_ids, ntpp, topk_weights_flat, *, T: int,
+            top_k: int, shared: MoeExperts | None = None, path: str | int = "auto") -> torch.Tensor:
+    lib = _lib.load()
+    p = _path(path)
+    bm = _block_m(p, T, top_k)
+    ys = torch.empty(h.shape[0], experts.hidden_size, dtype=torch.float32, device=h.device)
+    ex = experts.struct()
+    sh = shared.struct() if shared is not None else None
+    _lib.check(lib.moe_w2_down_v1(
+        h.data_ptr(), T, top_k, ctypes.byref(ex), ctypes.byref(sh) if sh else None,
+        sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(), bm, expert_ids.numel(),
+        topk_weights_flat.data_ptr(), ys.data_ptr(), p, _stream()))
+    return ys
+
+
+def moe_sum(ys: torch.Tensor, T: int, top_k: int, has_shared: bool = False) -> torch.Tensor:
+    lib = _lib.load()
+    H = ys.shape[1]
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=ys.device)
+    _lib.check(lib.moe_sum_v1(ys.data_ptr(), T, top_k, H, int(has_shared), out.data_ptr(), _stream()))
+    return out
+
+
+# ----------------------------------------------------------------------------- whole layer
+def workspace_bytes(T: int, top_k: int, experts: MoeExperts, has_shared: bool,
+                    path: str | int = "auto") -> int:
+    ex = experts.struct()
+    n = int(_lib.load().moe_layer_workspace_bytes_v1(T, top_k, ctypes.byref(ex), int(has_shared),
+                                                     _path(path)))
+    if n < 0:
+        raise ValueError("invalid sizes for the workspace query")
+    return n
+
+
+def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, top_k: int = 8,
+              logit_bias: torch.Tensor | None = None, shared: MoeExperts | None = None,
+              shared_gate_w: torch.Tensor | None = None, path: str | int = "auto",
+              workspace: torch.Tensor | None = None, return_routing: bool = False):
+    """Routed MoE layer: router -> align -> W1 -> W2 -> sum (+ gated shared expert)."""
+    lib = _lib.load()
+    _bf16_matrix(x, "input", experts.hidden_size)
+    _bf16_matrix(router_w, "router_w", experts.hidden_size)
+    if router_w.shape[0] != experts.num_experts:
+        raise ValueError(f"router_w has {router_w.shape[0]} rows for {experts.num_experts} experts")
+    if (shared is None) != (shared_gate_w is None):
+        raise ValueError("shared and shared_gate_w must be given together")
+    _require_gpu(x, router_w, logit_bias, shared_gate_w, experts.gate.qweight)
+    T = x.shape[0]
+    p = _path(path)
+    need = workspace_bytes(T, top_k, experts, shared is not None, p)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty_like(x)
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device) if return_routing else None
+    w = torch.empty(T, top_k, dtype=torch.float32, device=x.device) if return_routing else None
+    ex = experts.struct()
+    sh = shared.struct() if shared is not None else None
+    _lib.check(lib.moe_layer_v1(
+        x.data_ptr(), T, router_w.data_ptr(), _ptr(logit_bias), top_k, ctypes.byref(ex),
+        ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
+        workspace.numel(), out.data_ptr(), _ptr(ids), _ptr(w), p, _stream()))
+    if return_routing:
+        return out, ids, w
+    return out
+
+
+def fused_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                  experts: MoeExperts, *, shared: MoeExperts | None = None,
+                  shared_gate_w: torch.Tensor | None = None, path: str | int = "auto",
+                  workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Experts with caller-given routing (ids int32 [T, k], weights fp32 [T, k])."""
+    lib = _lib.load()
+    _bf16_matrix(x, "input", experts.hidden_size)
+    if topk_ids.dtype != torch.int32 or topk_weights.dtype != torch.float32:
+        raise TypeError("topk_ids must be int32 and topk_weights float32")
+    if topk_ids.shape != topk_weights.shape or topk_ids.ndim != 2 or topk_ids.shape[0] != x.shape[0]:
+        raise ValueError("topk_ids/topk_weights must be [T, k] matching the input rows")
+    if (shared is None) != (shared_gate_w is None):
+        raise ValueError("shared and shared_gate_w must be given together")
+    _require_gpu(x, topk_ids, topk_weights, shared_gate_w, experts.gate.qweight)
+    T, k = topk_ids.shape
+    p = _path(path)
+    need = workspace_bytes(T, k, experts, shared is not None, p)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty_like(x)
+    ex = experts.struct()
+    sh = shared.struct() if shared is not None else None
+    _lib.check(lib.moe_fused_experts_v1(
+        x.data_ptr(), T, topk_ids.data_ptr(), topk_weights.data_ptr(), k, ctypes.byref(ex),
+        ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
+        workspace.numel(), out.data_ptr(), p, _stream()))
+    return out

@@ -1,0 +1,78 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the header declares,
+and its host-side validation returns the documented error codes (no kernel is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mtp_amd import _lib
+from oracle import moe_ref
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "moe_w4a16.h"
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^(?:int|int64_t|const char\*)\s+(moe_[a-z0-9_]+)\(", text, flags=re.M)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = header_functions()
+    assert declared, "no declarations parsed from the header"
+    assert sorted(declared) == sorted(_lib.EXPORTED)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.moe_w4a16_abi_version() == _lib.ABI_VERSION
+
+
+def _fake_set(E=256, H=2048, I=512, G=128) -> _lib.ExpertSet:
+    p = _lib.GptqProj(0x1000, 0x2000, 0x3000)  # never dereferenced by the host-side checks
+    return _lib.ExpertSet(p, p, p, None, E, H, I, G)
+
+
+def test_null_and_shape_errors_are_reported():
+    lib = _lib.load()
+    rc = lib.moe_layer_v1(None, 4, None, None, 8, None, None, None, None, 0, None, None, None, 0, None)
+    assert rc == _lib.MOE_ERR_NULL
+    assert b"experts is NULL" in lib.moe_w4a16_last_error()
+    bad = _fake_set(H=1000)
+    rc = lib.moe_w1_gateup_silu_v1(None, 4, 8, ctypes.byref(bad), None, None, None, None, 16, 1,
+                                   None, 0, None)
+    assert rc == _lib.MOE_ERR_SHAPE
+    with pytest.raises(_lib.MoeLibraryError) as err:
+        _lib.check(rc)
+    assert err.value.code == _lib.MOE_ERR_SHAPE and "hidden=1000" in str(err.value)
+    rc = lib.moe_router_topk_v1(0x10, 1, 2048, 0x10, 256, None, 300, None, 0x10, 0x10, 0x10, None)
+    assert rc == _lib.MOE_ERR_SHAPE
+    rc = lib.moe_align_v1(0x10, 4, 8, 256, 0, 16, 1, 0x10, 0x10, 0x10, None)
+    assert rc == _lib.MOE_ERR_WORKSPACE
+
+
+def test_workspace_too_small_is_rejected():
+    lib = _lib.load()
+    ex = _fake_set()
+    need = lib.moe_layer_workspace_bytes_v1(16, 8, ctypes.byref(ex), 0, 0)
+    assert need > 0
+    rc = lib.moe_layer_v1(0x10, 16, 0x10, None, 8, ctypes.byref(ex), None, None, 0x10, need - 1,
+                          0x10, None, None, 0, None)
+    assert rc == _lib.MOE_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("T,k,E,shared,BM", [(1, 8, 256, 0, 16), (64, 8, 256, 1, 16),
+                                               (2048, 8, 256, 0, 128), (3, 4, 16, 1, 4)])
+def test_capacity_blocks_matches_oracle_bound(T, k, E, shared, BM):
+    lib = _lib.load()
+    got = lib.moe_capacity_blocks_v1(T, k, E, shared, BM)
+    assert got == moe_ref.max_blocks(T * k + (T if shared else 0), E + shared, BM)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setenv("MTP_AMD_LIB", str(tmp_path / "absent.so"))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _lib.load()

@@ -1,0 +1,126 @@
+"""GPU parity of the fused W4A16 MoE layer against the fp32-accumulated oracle.
+
+Routing ids must be bit-exact; layer outputs within LAYER_RTOL (1e-2) normwise relative error
+max|out - ref| / max|ref| (bf16 output against an fp32-accumulated reference that uses the
+reference's bit-exact bf16 dequantised weights).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mtp_amd import ops, synth
+from mtp_amd.moe import MoeBlock
+from oracle import moe_ref
+from tests.helpers import LAYER_RTOL, bf16_bits, experts_to_np, small_layer, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def _check_layer(layer_cpu, T, top_k, path, seed=7):
+    x = synth.make_tokens(T, layer_cpu.experts.hidden_size, seed=seed)
+    g = to_gpu(layer_cpu)
+    out, ids, w = ops.moe_layer(x.cuda(), g.router_w, g.experts, top_k=top_k,
+                                logit_bias=g.logit_bias, shared=g.shared,
+                                shared_gate_w=g.shared_gate_w, path=path, return_routing=True)
+    torch.cuda.synchronize()
+    ref, r_ids, r_w, _ = moe_ref.moe_layer_ref(
+        bf16_bits(x), bf16_bits(layer_cpu.router_w), experts_to_np(layer_cpu.experts), top_k=top_k,
+        logit_bias=None if layer_cpu.logit_bias is None else layer_cpu.logit_bias.numpy(),
+        shared=None if layer_cpu.shared is None else experts_to_np(layer_cpu.shared),
+        shared_gate_w_bits=None if layer_cpu.shared_gate_w is None else bf16_bits(layer_cpu.shared_gate_w))
+    assert np.array_equal(ids.cpu().numpy(), r_ids), "routing ids must be bit-exact"
+    np.testing.assert_allclose(w.cpu().numpy(), r_w, rtol=2e-6, atol=1e-7)
+    err = moe_ref.rel_err(out.float().cpu().numpy(), ref)
+    _say(f"  rel_err={err:.3e}")
+    assert err <= LAYER_RTOL
+    return out
+
+
+@pytest.mark.parametrize("T", [1, 3, 16])
+@pytest.mark.parametrize("path", ["decode", "prefill"])
+def test_small_layer(T, path):
+    _say(f"small layer T={T} path={path}")
+    _check_layer(small_layer(0), T, 4, path)
+
+
+@pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode")])
+def test_config1_full_shape(T, path):
+    """Config 1: hidden 2048, 256 experts, intermediate 512, top-8, 16 tokens."""
+    _say(f"config1 T={T} path={path}")
+    _check_layer(synth.make_layer(0), T, 8, path)
+
+
+@pytest.mark.parametrize("T", [1, 32])
+def test_config4_shared_expert(T):
+    """Config 4: routed top-8 plus a sigmoid-gated int4 shared expert."""
+    _say(f"config4 T={T}")
+    _check_layer(synth.make_layer(1, shared=True), T, 8, "auto")
+
+
+def test_decode_and_prefill_paths_agree_on_zipf_batch():
+    _say("decode vs prefill T=64 zipf")
+    layer = to_gpu(synth.make_layer(2, zipf=True))
+    x = synth.make_tokens(64, seed=11).cuda()
+    a = ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias, path="decode")
+    b = ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias, path="prefill")
+    assert moe_ref.rel_err(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-2
+
+
+def test_fused_experts_and_moe_tokens_api():
+    _say("moe_tokens API")
+    layer = small_layer(3, shared=True)
+    g = to_gpu(layer)
+    T, k = 6, 4
+    x = synth.make_tokens(T, 512, seed=3)
+    rng = np.random.default_rng(0)
+    ids = np.stack([rng.choice(16, k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[0, 1] = ids[0, 0]  # a duplicated expert in one token is summed twice
+    w = rng.uniform(0.05, 0.5, (T, k)).astype(np.float32)
+    block = MoeBlock(g.experts, g.router_w, shared_expert=g.shared,
+                     shared_expert_gate_weight=g.shared_gate_w, top_k=k)
+    out = block.moe_tokens(x.cuda().view(2, 3, 512), torch.from_numpy(ids).view(2, 3, k),
+                           torch.from_numpy(w).view(2, 3, k))
+    sg = moe_ref.shared_gate(bf16_bits(x), bf16_bits(layer.shared_gate_w))
+    ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(layer.experts),
+                                shared=experts_to_np(layer.shared), shared_gate_values=sg)
+    assert moe_ref.rel_err(out.view(T, 512).float().cpu().numpy(), ref) <= LAYER_RTOL
+    with pytest.raises(KeyError):
+        block.moe_tokens(x.cuda().view(2, 3, 512), torch.full((2, 3, k), 99), torch.from_numpy(w).view(2, 3, k))
+
+
+def test_expert_row_indirection_matches_direct():
+    """A slot pool: experts held in arbitrary rows, addressed through expert_row."""
+    _say("expert_row indirection")
+    layer = to_gpu(small_layer(4))
+    E = 16
+    perm = torch.randperm(E, generator=torch.Generator().manual_seed(1))
+    from mtp_amd.weights import GptqStack, MoeExperts
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(E)
+
+    def permute(st: GptqStack) -> GptqStack:
+        return GptqStack(st.qweight[perm.cuda()].contiguous(), st.qzeros[perm.cuda()].contiguous(),
+                         st.scales[perm.cuda()].contiguous())
+    pooled = MoeExperts(permute(layer.experts.gate), permute(layer.experts.up),
+                        permute(layer.experts.down), 128,
+                        expert_row=inv.to(torch.int32).cuda(), num_experts=E)
+    x = synth.make_tokens(9, 512, seed=4).cuda()
+    for path in ("decode", "prefill"):
+        a = ops.moe_layer(x, layer.router_w, layer.experts, top_k=4, path=path)
+        b = ops.moe_layer(x, layer.router_w, pooled, top_k=4, path=path)
+        assert torch.equal(a, b)
+
+
+def test_layer_is_deterministic():
+    _say("determinism")
+    layer = to_gpu(synth.make_layer(5, zipf=True))
+    x = synth.make_tokens(32, seed=5).cuda()
+    outs = [ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias) for _ in range(3)]
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
