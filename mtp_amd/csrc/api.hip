@@ -46,7 +46,7 @@ int check_experts(const moe_expert_set_v1* ex, const moe_expert_set_v1* sh) {
     return fail(MOE_ERR_SHAPE, "hidden=%d must be a multiple of 512 in [512, 2048]", H);
   if (!(I == 256 || I == 512 || I == 1024))
     return fail(MOE_ERR_SHAPE, "intermediate=%d must be one of 256, 512, 1024", I);
-  if (G < 64 || G % 64 != 0 || H % G != 0 || I % G != 0)
+  if (!(G == 64 || G == 128 || G == 256) || H % G != 0 || I % G != 0)
     return fail(MOE_ERR_SHAPE, "group_size=%d unsupported for hidden=%d intermediate=%d", G, H,
                 I);
   if (sh) {
@@ -77,11 +77,28 @@ ExpertsDev make_experts_dev(const moe_expert_set_v1* ex, const moe_expert_set_v1
 }
 
 int resolve_path(int path, int T, int top_k) {
-  if (path == MOE_PATH_DECODE || path == MOE_PATH_PREFILL) return path;
+  if (path == MOE_PATH_DECODE || path == MOE_PATH_PREFILL || path == MOE_PATH_GEMV) return path;
   return (T * top_k >= 1024) ? MOE_PATH_PREFILL : MOE_PATH_DECODE;
 }
 
 int block_m_of(int path) { return path == MOE_PATH_PREFILL ? kPrefillBlockM : kDecodeBlockM; }
+
+hipError_t dispatch_w1(int path, const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int bm,
+                       int cap, uint16_t* h, hipStream_t s) {
+  if (path == MOE_PATH_PREFILL) return launch_w1_prefill(x, ed, sd, sorted, eids, ntpp, bm, cap, h, s);
+  if (path == MOE_PATH_GEMV) return launch_w1_decode(x, ed, sd, sorted, eids, ntpp, bm, cap, h, s);
+  return launch_w1_decode_mfma(x, ed, sd, sorted, eids, ntpp, cap, h, s);
+}
+
+hipError_t dispatch_w2(int path, const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int bm,
+                       int cap, const float* w, float* ys, hipStream_t s) {
+  if (path == MOE_PATH_PREFILL)
+    return launch_w2_prefill(h, ed, sd, sorted, eids, ntpp, bm, cap, w, ys, s);
+  if (path == MOE_PATH_GEMV) return launch_w2_decode(h, ed, sd, sorted, eids, ntpp, bm, cap, w, ys, s);
+  return launch_w2_decode_mfma(h, ed, sd, sorted, eids, ntpp, cap, w, ys, s);
+}
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -128,17 +145,8 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   float* ys = at<float>(ws, L.ys);
   MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted, eids,
                              ntpp, stream), "align");
-  if (path == MOE_PATH_PREFILL) {
-    MOE_CHECK_HIP(launch_w1_prefill(x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream),
-                  "w1 prefill");
-    MOE_CHECK_HIP(launch_w2_prefill(h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
-                  "w2 prefill");
-  } else {
-    MOE_CHECK_HIP(launch_w1_decode(x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream),
-                  "w1 decode");
-    MOE_CHECK_HIP(launch_w2_decode(h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
-                  "w2 decode");
-  }
+  MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream), "w1");
+  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream), "w2");
   MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, out, stream), "moe_sum");
   return MOE_OK;
 }
@@ -235,13 +243,8 @@ int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
                 block_m_of(path));
   const ExpertsDev ed = make_experts_dev(experts, shared);
   const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
-  hipStream_t s = (hipStream_t)stream;
-  if (path == MOE_PATH_PREFILL)
-    MOE_CHECK_HIP(launch_w1_prefill(x, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
-                                    capacity_blocks, h, s), "w1 prefill");
-  else
-    MOE_CHECK_HIP(launch_w1_decode(x, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
-                                   capacity_blocks, h, s), "w1 decode");
+  MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+                            capacity_blocks, h, (hipStream_t)stream), "w1");
   return MOE_OK;
 }
 
@@ -262,13 +265,8 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
                 block_m_of(path));
   const ExpertsDev ed = make_experts_dev(experts, shared);
   const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
-  hipStream_t s = (hipStream_t)stream;
-  if (path == MOE_PATH_PREFILL)
-    MOE_CHECK_HIP(launch_w2_prefill(h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
-                                    capacity_blocks, topk_weights, ys, s), "w2 prefill");
-  else
-    MOE_CHECK_HIP(launch_w2_decode(h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
-                                   capacity_blocks, topk_weights, ys, s), "w2 decode");
+  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+                            capacity_blocks, topk_weights, ys, (hipStream_t)stream), "w2");
   return MOE_OK;
 }
 

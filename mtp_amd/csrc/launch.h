@@ -24,7 +24,15 @@ hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int ha
                         int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp,
                         hipStream_t stream);
 
-// Decode (VALU GEMV) path.
+// Decode path on MFMA with in-register dequantisation (blocks of kDecodeBlockM slots).
+hipError_t launch_w1_decode_mfma(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                                 const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                                 int cap, uint16_t* h, hipStream_t stream);
+hipError_t launch_w2_decode_mfma(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                                 const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                                 int cap, const float* topk_w, float* ys, hipStream_t stream);
+
+// Decode path on VALU dot products (v_dot2_f32_bf16) with shuffle K-reduction.
 hipError_t launch_w1_decode(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                             const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                             int BM, int cap, uint16_t* h, hipStream_t stream);

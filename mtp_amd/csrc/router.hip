@@ -9,15 +9,17 @@
 // 8 elements in increasing k with fma from +0.0f (bf16*bf16 products are exact in fp32, so
 // fma == add of the product); the 64 partials are combined by v += shfl_xor(v, m) for
 // m = 32, 16, 8, 4, 2, 1. Ties in top-k: larger logit first, then lower expert id.
+//
+// The logits kernel tiles TT tokens x TE router rows per wave (small tiles at decode for more
+// waves in flight, 8 x 8 at prefill for register reuse); the tile shape never changes the
+// per-(token, row) summation order.
 #include "common.h"
 #include "launch.h"
 
 namespace {
 
-constexpr int TT = 4;  // tokens per wave tile
-constexpr int TE = 4;  // router rows per wave tile
-
 // logits[t, row] for rows 0..E-1 (router_w) and, if shared_w, row E (shared gate).
+template <int TT, int TE>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ W, int E,
     const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
@@ -35,6 +37,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     const int e = e0 + j;
     wrow[j] = e < E ? W + (int64_t)e * H : (e == E && shared_w ? shared_w : nullptr);
   }
+  const uint16_t* xrow[TT];
+#pragma unroll
+  for (int i = 0; i < TT; ++i) xrow[i] = (t0 + i < T) ? x + (int64_t)(t0 + i) * H : nullptr;
   float acc[TT][TE];
 #pragma unroll
   for (int i = 0; i < TT; ++i)
@@ -42,25 +47,25 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
 
   const int nq = H / 8;
+#pragma unroll 4
   for (int q = lane; q < nq; q += 64) {
     u32x4 xv[TT], wv[TE];
 #pragma unroll
-    for (int i = 0; i < TT; ++i)
-      xv[i] = (t0 + i < T) ? ld128(x + (int64_t)(t0 + i) * H + 8 * q) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < TT; ++i) xv[i] = xrow[i] ? ld128(xrow[i] + 8 * q) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < TE; ++j) wv[j] = wrow[j] ? ld128(wrow[j] + 8 * q) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int el = 0; el < 8; ++el) {
+      float wf[TE];
+#pragma unroll
+      for (int j = 0; j < TE; ++j)
+        wf[j] = (el & 1) ? bf16hi_to_f32(wv[j][el >> 1]) : bf16lo_to_f32(wv[j][el >> 1]);
 #pragma unroll
       for (int i = 0; i < TT; ++i) {
         const uint32_t xd = xv[i][el >> 1];
         const float xf = (el & 1) ? bf16hi_to_f32(xd) : bf16lo_to_f32(xd);
 #pragma unroll
-        for (int j = 0; j < TE; ++j) {
-          const uint32_t wd = wv[j][el >> 1];
-          const float wf = (el & 1) ? bf16hi_to_f32(wd) : bf16lo_to_f32(wd);
-          acc[i][j] = __builtin_fmaf(xf, wf, acc[i][j]);
-        }
+        for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xf, wf[j], acc[i][j]);
       }
     }
   }
@@ -92,7 +97,41 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
-// One wave per token: iterative arg-max with (value desc, id asc) ordering.
+// Total order on (logit, expert): larger logit first, then lower id. NaN never outranks.
+MOE_DEV uint64_t topk_key(float v, int e) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if ((__float_as_uint(v) & 0x7FFFFFFFu) > 0x7F800000u) u = 0;  // NaN ranks last
+  return ((uint64_t)u << 32) | (uint32_t)(~(uint32_t)e);
+}
+
+#define MOE_DPP(v, ctrl, rmask) \
+  (uint32_t) __builtin_amdgcn_update_dpp((int)(v), (int)(v), ctrl, rmask, 0xF, false)
+
+MOE_DEV uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Wave-wide maximum of a 64-bit key through DPP (quad xor 1, quad xor 2, half-row mirror, row
+// mirror, row_bcast15, row_bcast31); the result is read from lane 63 and is wave-uniform.
+MOE_DEV uint64_t wave_max_u64(uint64_t v) {
+#define MOE_DPP_STEP(ctrl, rmask)                                                     \
+  do {                                                                                \
+    const uint32_t lo = MOE_DPP((uint32_t)v, ctrl, rmask);                            \
+    const uint32_t hi = MOE_DPP((uint32_t)(v >> 32), ctrl, rmask);                    \
+    v = max_u64(v, ((uint64_t)hi << 32) | lo);                                        \
+  } while (0)
+  MOE_DPP_STEP(0xB1, 0xF);   // quad_perm(1,0,3,2)
+  MOE_DPP_STEP(0x4E, 0xF);   // quad_perm(2,3,0,1)
+  MOE_DPP_STEP(0x141, 0xF);  // row_half_mirror
+  MOE_DPP_STEP(0x140, 0xF);  // row_mirror
+  MOE_DPP_STEP(0x142, 0xA);  // row_bcast15 into rows 1, 3
+  MOE_DPP_STEP(0x143, 0xC);  // row_bcast31 into rows 2, 3
+#undef MOE_DPP_STEP
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// One wave per token: top_k rounds of a wave-wide arg-max over (value desc, id asc).
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T,
                                                           int E, int top_k, int has_shared,
                                                           int32_t* __restrict__ ids,
@@ -102,46 +141,26 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   if (t >= T) return;
   constexpr int MAXC = 8;  // E <= 512
   const float* row = logits + (int64_t)t * (E + 1);
-  float v[MAXC];
-  bool taken[MAXC];
+  uint64_t key[MAXC];
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int e = lane + 64 * c;
-    v[c] = e < E ? row[e] : 0.0f;
-    taken[c] = !(e < E);
+    key[c] = e < E ? topk_key(row[e], e) : 0ull;
   }
   float my_v = 0.0f;
   int my_i = 0;
   for (int r = 0; r < top_k; ++r) {
-    float bv = -__builtin_huge_valf();
-    int bi = 0x7fffffff;
+    uint64_t head = 0;
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int e = lane + 64 * c;
-      if (!taken[c] && (bi == 0x7fffffff || v[c] > bv || (v[c] == bv && e < bi))) {
-        bv = v[c];
-        bi = e;
-      }
-    }
+    for (int c = 0; c < MAXC; ++c) head = max_u64(head, key[c]);
+    const uint64_t best = wave_max_u64(head);
+    const int e = (int)(~(uint32_t)best);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
-      const bool other_better =
-          (oi != 0x7fffffff) && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-      if (other_better) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi != 0x7fffffff && (bi & 63) == lane) {
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c)
-        if (c == (bi >> 6)) taken[c] = true;
-    }
+    for (int c = 0; c < MAXC; ++c)
+      if (key[c] == best) key[c] = 0ull;  // exactly one lane/slot holds the unique key
     if (lane == r) {
-      my_v = bv;
-      my_i = bi;
+      my_i = e;
+      my_v = row[e];
     }
   }
   const float vmax = __shfl(my_v, 0, 64);
@@ -158,18 +177,27 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   }
 }
 
+template <int TT, int TE>
+hipError_t launch_logits_tiled(const uint16_t* x, int T, int H, const uint16_t* W, int E,
+                               const uint16_t* shared_w, const float* bias, float* logits,
+                               hipStream_t stream) {
+  const int rows = E + (shared_w ? 1 : 0);
+  const int tiles = ((T + TT - 1) / TT) * ((rows + TE - 1) / TE);
+  const int blocks = (tiles + 3) / 4;
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL((router_logits_kernel<TT, TE>), dim3(blocks), dim3(256), 0, stream, x, T, H,
+                     W, E, shared_w, bias, logits);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t* W, int E,
                                 const uint16_t* shared_w, const float* bias, float* logits,
                                 hipStream_t stream) {
-  const int rows = E + (shared_w ? 1 : 0);
-  const int tiles = ((T + TT - 1) / TT) * ((rows + TE - 1) / TE);
-  const int blocks = (tiles + 3) / 4;
-  if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(router_logits_kernel, dim3(blocks), dim3(256), 0, stream, x, T, H, W, E,
-                     shared_w, bias, logits);
-  return hipGetLastError();
+  if (T <= 4) return launch_logits_tiled<1, 2>(x, T, H, W, E, shared_w, bias, logits, stream);
+  if (T <= 64) return launch_logits_tiled<2, 4>(x, T, H, W, E, shared_w, bias, logits, stream);
+  return launch_logits_tiled<8, 8>(x, T, H, W, E, shared_w, bias, logits, stream);
 }
 
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,

@@ -14,7 +14,8 @@ import torch
 from mtp_amd import _lib
 from mtp_amd.weights import MoeExperts
 
-PATHS = {"auto": _lib.PATH_AUTO, "decode": _lib.PATH_DECODE, "prefill": _lib.PATH_PREFILL}
+PATHS = {"auto": _lib.PATH_AUTO, "decode": _lib.PATH_DECODE, "prefill": _lib.PATH_PREFILL,
+         "gemv": _lib.PATH_GEMV}
 DECODE_BLOCK_M = 16
 PREFILL_BLOCK_M = 128
 OUT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -210,7 +211,8 @@ def workspace_bytes(T: int, top_k: int, experts: MoeExperts, has_shared: bool,
 def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, top_k: int = 8,
               logit_bias: torch.Tensor | None = None, shared: MoeExperts | None = None,
               shared_gate_w: torch.Tensor | None = None, path: str | int = "auto",
-              workspace: torch.Tensor | None = None, return_routing: bool = False):
+              workspace: torch.Tensor | None = None, return_routing: bool = False,
+              out: torch.Tensor | None = None):
     """Routed MoE layer: router -> align -> W1 -> W2 -> sum (+ gated shared expert)."""
     lib = _lib.load()
     _bf16_matrix(x, "input", experts.hidden_size)
@@ -225,7 +227,10 @@ def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, t
     need = workspace_bytes(T, top_k, experts, shared is not None, p)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
-    out = torch.empty_like(x)
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor shaped like the input")
     ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device) if return_routing else None
     w = torch.empty(T, top_k, dtype=torch.float32, device=x.device) if return_routing else None
     ex = experts.struct()

@@ -28,7 +28,7 @@ ZIPF_S = 1.1
 # Logit bias scale: b[perm[i]] = ZIPF_TAU * ln(p_i), p_i ~ i^-1.1, calibrated so the realised
 # per-expert top-8 selection frequencies over 65536 tokens best fit Zipf(1.1)
 # (mtp_amd/calibrate_zipf.py writes this value).
-ZIPF_TAU = 1.0
+ZIPF_TAU = 0.5
 
 
 def _gen(seed: int, device) -> torch.Generator:

@@ -220,6 +220,24 @@ def rel_err(out: np.ndarray, ref: np.ndarray) -> float:
 
 
 # --------------------------------------------------------------------------- faithful bf16 path
+def dequant_stack_torch(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                        group_size: int = 128) -> torch.Tensor:
+    """Vectorised CPU dequant of stacked experts -> bf16 Linear weights [n, N, K].
+
+    Same formula as gptq_ref.dequant_bf16_bits (gptq_unpack.py:88-131), in torch for speed;
+    pinned bit-for-bit against the numpy restatement in tests/test_oracle_moe.py."""
+    n, k8, cols = qweight.shape
+    u = qweight.to(torch.int64) & 0xFFFFFFFF
+    shifts = torch.arange(8, dtype=torch.int64) * 4
+    q = ((u[:, :, None, :] >> shifts[None, None, :, None]) & 0xF).reshape(n, k8 * 8, cols)
+    zu = qzeros.to(torch.int64) & 0xFFFFFFFF
+    z = ((zu[:, :, :, None] >> shifts[None, None, None, :]) & 0xF).reshape(n, qzeros.shape[1], cols)
+    g = torch.arange(k8 * 8) // group_size
+    w = (q.to(torch.float32) - z.to(torch.float32)[:, g, :]) * scales.to(torch.float32)[:, g, :]
+    return w.transpose(1, 2).contiguous().to(torch.bfloat16)
+
+
+
 def moe_tokens_bf16(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                     experts: dict[int, tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
                     shared: tuple | None = None, shared_gate_w: torch.Tensor | None = None) -> torch.Tensor:

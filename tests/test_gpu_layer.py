@@ -43,14 +43,15 @@ def _check_layer(layer_cpu, T, top_k, path, seed=7):
     return out
 
 
-@pytest.mark.parametrize("T", [1, 3, 16])
-@pytest.mark.parametrize("path", ["decode", "prefill"])
+@pytest.mark.parametrize("T", [1, 3, 16, 40])
+@pytest.mark.parametrize("path", ["decode", "prefill", "gemv"])
 def test_small_layer(T, path):
     _say(f"small layer T={T} path={path}")
     _check_layer(small_layer(0), T, 4, path)
 
 
-@pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode")])
+@pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode"), (16, "gemv"),
+                                    (64, "decode")])
 def test_config1_full_shape(T, path):
     """Config 1: hidden 2048, 256 experts, intermediate 512, top-8, 16 tokens."""
     _say(f"config1 T={T} path={path}")
@@ -68,9 +69,10 @@ def test_decode_and_prefill_paths_agree_on_zipf_batch():
     _say("decode vs prefill T=64 zipf")
     layer = to_gpu(synth.make_layer(2, zipf=True))
     x = synth.make_tokens(64, seed=11).cuda()
-    a = ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias, path="decode")
-    b = ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias, path="prefill")
-    assert moe_ref.rel_err(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-2
+    outs = [ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias, path=p)
+            for p in ("decode", "prefill", "gemv")]
+    for o in outs[1:]:
+        assert moe_ref.rel_err(o.float().cpu().numpy(), outs[0].float().cpu().numpy()) < 1e-2
 
 
 def test_fused_experts_and_moe_tokens_api():
@@ -112,7 +114,7 @@ def test_expert_row_indirection_matches_direct():
                         permute(layer.experts.down), 128,
                         expert_row=inv.to(torch.int32).cuda(), num_experts=E)
     x = synth.make_tokens(9, 512, seed=4).cuda()
-    for path in ("decode", "prefill"):
+    for path in ("decode", "prefill", "gemv"):
         a = ops.moe_layer(x, layer.router_w, layer.experts, top_k=4, path=path)
         b = ops.moe_layer(x, layer.router_w, pooled, top_k=4, path=path)
         assert torch.equal(a, b)

@@ -62,6 +62,18 @@ def test_f32_oracle_agrees_with_reference_bf16_flow():
     assert moe_ref.rel_err(out16.float().numpy(), ref32) < 2e-2
 
 
+def test_torch_stack_dequant_matches_numpy_restatement():
+    layer = _layer_np(3, 256, 128, 4)
+    for proj in ("gate_proj", "down_proj"):
+        got = moe_ref.dequant_stack_torch(torch.from_numpy(layer[f"{proj}.qweight"]),
+                                          torch.from_numpy(layer[f"{proj}.qzeros"]),
+                                          torch.from_numpy(layer[f"{proj}.scales"].view(np.float16)))
+        for e in range(3):
+            want = gptq_ref.dequant_bf16_bits(layer[f"{proj}.qweight"][e], layer[f"{proj}.qzeros"][e],
+                                              layer[f"{proj}.scales"][e])
+            assert np.array_equal(got[e].view(torch.int16).numpy().view(np.uint16), want)
+
+
 def test_rel_err_metric():
     ref = np.array([1.0, -4.0, 2.0])
     assert abs(moe_ref.rel_err(ref + np.array([0.0, 0.04, 0.0]), ref) - 0.01) < 1e-12
