@@ -107,7 +107,7 @@ def main() -> int:
     for T in batches:
         x = synth.make_tokens(T, seed=7, device=dev)
         need = ops.workspace_bytes(T, K, layers[0].experts, False, args.decode_path)
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
         outs = [torch.empty(T, H, dtype=torch.bfloat16, device=dev) for _ in range(L)]
         uniq = []
         for l, ly in enumerate(layers):
@@ -215,7 +215,7 @@ def main() -> int:
         ly = layers[0]
         xp = synth.make_tokens(Tp, seed=7, device=dev)
         need = ops.workspace_bytes(Tp, K, ly.experts, False, "auto")
-        wsp = torch.empty(need, dtype=torch.uint8, device=dev)
+        wsp = torch.zeros(need, dtype=torch.uint8, device=dev)
         outp = torch.empty(Tp, H, dtype=torch.bfloat16, device=dev)
         _, ids, _ = ops.moe_layer(xp, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
                                   workspace=wsp, out=outp, return_routing=True)

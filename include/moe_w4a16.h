@@ -139,7 +139,8 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
 int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
                uint16_t* out, void* stream);
 
-/* Workspace bytes for moe_layer_v1 / moe_fused_experts_v1. */
+/* Workspace bytes for moe_layer_v1 / moe_fused_experts_v1 (no state survives between calls;
+ * calls that share one workspace must be ordered on one stream). */
 int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_set_v1* experts,
                                      int32_t has_shared, int32_t path);
 

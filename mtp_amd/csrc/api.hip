@@ -3,6 +3,7 @@
 // synchronises the host.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 
 #include "common.h"
 #include "launch.h"
@@ -102,6 +103,7 @@ hipError_t dispatch_w2(int path, const uint16_t* h, const ExpertsDev& ed, const 
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Workspace of moe_layer_v1 / moe_fused_experts_v1 (no state survives between calls).
 struct Workspace {
   size_t logits, ids, w, sorted, eids, ntpp, h, ys, total;
   int cap, bm;
@@ -129,10 +131,11 @@ Workspace layout(int T, int top_k, const moe_expert_set_v1* ex, int has_shared, 
 template <typename T>
 T* at(void* base, size_t off) { return reinterpret_cast<T*>(static_cast<char*>(base) + off); }
 
-// align -> W1 -> W2 -> sum over a routed workspace (ids and weights already in place).
+// [align ->] W1 -> W2 -> top-k sum over a routed workspace (ids and weights in place; when
+// `aligned` the sorted slot layout is in place too).
 int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex,
                 const moe_expert_set_v1* sh, const Workspace& L, void* ws, uint16_t* out,
-                int path, hipStream_t stream) {
+                int path, bool aligned, hipStream_t stream) {
   const int has_shared = sh ? 1 : 0;
   const ExpertsDev ed = make_experts_dev(ex, sh);
   SlotsDev sd{T, top_k, T * top_k + (has_shared ? T : 0)};
@@ -143,10 +146,12 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   int32_t* ntpp = at<int32_t>(ws, L.ntpp);
   uint16_t* h = at<uint16_t>(ws, L.h);
   float* ys = at<float>(ws, L.ys);
-  MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted, eids,
-                             ntpp, stream), "align");
+  if (!aligned)
+    MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
+                               eids, ntpp, stream), "align");
   MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream), "w1");
-  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream), "w2");
+  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
+                "w2");
   MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, out, stream), "moe_sum");
   return MOE_OK;
 }
@@ -266,7 +271,8 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
   const ExpertsDev ed = make_experts_dev(experts, shared);
   const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
   MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
-                            capacity_blocks, topk_weights, ys, (hipStream_t)stream), "w2");
+                            capacity_blocks, topk_weights, ys,
+                            (hipStream_t)stream), "w2");
   return MOE_OK;
 }
 
@@ -314,8 +320,17 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E,
                                      shared ? shared_gate_w : nullptr, logit_bias, logits, s),
                 "router logits");
-  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, shared ? 1 : 0, ids, w, s), "router topk");
-  rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, s);
+  // decode-size batches: top-k and align in one block (no align launch)
+  const bool topk_aligned = path != MOE_PATH_PREFILL && T <= kTopkAlignMaxTokens && top_k <= 8;
+  if (topk_aligned)
+    MOE_CHECK_HIP(launch_topk_align(logits, T, E, top_k, shared ? 1 : 0, L.bm, L.cap, ids, w,
+                                    at<int32_t>(workspace, L.sorted),
+                                    at<int32_t>(workspace, L.eids),
+                                    at<int32_t>(workspace, L.ntpp), s), "router topk+align");
+  else
+    MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, shared ? 1 : 0, ids, w, s),
+                  "router topk");
+  rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, topk_aligned, s);
   if (rc) return rc;
   if (topk_ids_out)
     MOE_CHECK_HIP(hipMemcpyAsync(topk_ids_out, ids, (size_t)T * top_k * 4,
@@ -353,7 +368,7 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
   if (shared)
     MOE_CHECK_HIP(launch_shared_gate(x, T, experts->hidden, shared_gate_w, top_k,
                                      at<float>(workspace, L.logits), w, s), "shared gate");
-  return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, s);
+  return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, false, s);
 }
 
 }  // extern "C"

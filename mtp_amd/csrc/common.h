@@ -80,6 +80,11 @@ struct ExpertsDev {
   int32_t hidden, inter, group;
 };
 
+// A block's expert id is usable: a routed expert, or the shared expert when one is present.
+MOE_DEV bool expert_ok(const ExpertsDev& ed, int e) {
+  return (e >= 0 && e < ed.num_experts) || (e == ed.num_experts && ed.sgate.qweight != nullptr);
+}
+
 MOE_DEV int64_t expert_row(const ExpertsDev& ed, int e) {
   return ed.expert_row ? (int64_t)ed.expert_row[e] : (int64_t)e;
 }
@@ -96,3 +101,4 @@ MOE_DEV int slot_token(const SlotsDev& s, int f) {
 }
 
 MOE_DEV float wave_xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(512) void gemm_decode_kernel(
   const int b = blockIdx.y;
   if (b * kBM >= *ntpp) return;
   const int e = eids[b];
-  if (e < 0) return;
+  if (!expert_ok(ed, e)) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(512) void gemm_decode_kernel(
   const int kw0 = wave * kKW;  // first k of this wave
   const int m = lane & 15, kq = lane >> 4;
   const int f_m = s_slot[m];
-  const bool valid_m = f_m < sd.num_slots;
+  const bool valid_m = (unsigned)f_m < (unsigned)sd.num_slots;
   const int64_t arow = valid_m ? ((MODE == DEC_W1) ? (int64_t)slot_token(sd, f_m) : (int64_t)f_m) : 0;
   const uint16_t* ap = act + arow * K + kw0 + 8 * kq;
   u32x4 av[kSteps];
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(512) void gemm_decode_kernel(
   for (int el = 0; el < 4; ++el) {
     const int r = 4 * (lane >> 4) + el;
     const int f = s_slot[r];
-    if (f >= sd.num_slots) continue;
+    if ((unsigned)f >= (unsigned)sd.num_slots) continue;
     if (MODE == DEC_W1) {
       const float h0 = silu_f32(acc[0][el]) * acc[2][el];
       const float h1 = silu_f32(acc[1][el]) * acc[3][el];

@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
   const int b = blockIdx.y;
   if (b * BM >= *ntpp) return;
   const int e = eids[b];
-  if (e < 0) return;
+  if (!expert_ok(ed, e)) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
     const int r = chunk >> 3;
     a_kc[i] = chunk & 7;
     const int f = s_slot[r];
-    if (f < sd.num_slots) {
+    if ((unsigned)f < (unsigned)sd.num_slots) {
       const int64_t arow = (MODE == MODE_W1) ? (int64_t)slot_token(sd, f) : (int64_t)f;
       a_row[i] = A + arow * K;
     } else {
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
     for (int el = 0; el < 4; ++el) {
       const int r = wm * 64 + mi * 16 + 4 * (lane >> 4) + el;
       const int f = s_slot[r];
-      if (f >= sd.num_slots) continue;
+      if ((unsigned)f >= (unsigned)sd.num_slots) continue;
       if (MODE == MODE_W1) {
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {

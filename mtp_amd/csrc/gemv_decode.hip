@@ -159,7 +159,7 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(const uint16_t* __rest
   const int b = blockIdx.y;
   if (b * BM >= *ntpp) return;
   const int e = eids[b];
-  if (e < 0) return;
+  if (!expert_ok(ed, e)) return;
   const int G = ed.group;
   const int K = (MODE == GEMV_W1) ? ed.hidden : ed.inter;
   const int NOUT = (MODE == GEMV_W1) ? ed.inter : ed.hidden;

@@ -16,6 +16,12 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
                                 hipStream_t stream);
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
                               int32_t* ids, float* weights, hipStream_t stream);
+// Top-k of every token and the align/sort in one 1024-thread block (T <= kTopkAlignMaxTokens,
+// top_k <= 8): the decode-size routing tail without a launch in between.
+constexpr int kTopkAlignMaxTokens = 8;
+hipError_t launch_topk_align(const float* logits, int T, int E, int top_k, int has_shared, int BM,
+                             int cap, int32_t* ids, float* weights, int32_t* sorted, int32_t* eids,
+                             int32_t* ntpp, hipStream_t stream);
 hipError_t launch_shared_gate(const uint16_t* x, int T, int H, const uint16_t* shared_w,
                               int top_k, float* logits_ws, float* weights, hipStream_t stream);
 

@@ -1,0 +1,271 @@
+// Device building blocks of the routing stage, shared by the standalone kernels (router.hip,
+// align.hip) and the fused decode routing kernel.
+//
+// logits_tile: fp32 logits of a TT x TE (token x router-row) tile by one wave in the canonical
+//   order (chunk q of 8 bf16 -> lane q % 64; per lane increasing q then k with fma from +0.0f;
+//   lanes combined by v += shfl_xor(v, m), m = 32 .. 1). The CPU oracle reproduces this order.
+// topk_token: one wave selects the top-k of one token's logits (larger logit first, equal logits
+//   -> lower id; vLLM topk_softmax(renormalize=True) semantics,
+//   src/mtp_expert_prefetch/tracing/vllm_router_trace.py:4201-4225).
+// align_block: one 1024-thread block turns top-k ids into the block-padded expert-grouped slot
+//   layout (vLLM moe_align_block_size format, vllm_router_trace.py:19647-19660): experts
+//   ascending, slots ascending inside an expert, each group padded to BM with the sentinel
+//   num_slots, unused blocks tagged -1.
+#pragma once
+
+#include "common.h"
+
+// ---------------------------------------------------------------------------- logits
+template <int TT, int TE>
+MOE_DEV void logits_tile(const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ W,
+                         int E, const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
+                         float* __restrict__ logits, int t0, int e0, int lane) {
+  const int rows = E + (shared_w ? 1 : 0);
+  const uint16_t* wrow[TE];
+#pragma unroll
+  for (int j = 0; j < TE; ++j) {
+    const int e = e0 + j;
+    wrow[j] = e < E ? W + (int64_t)e * H : (e == E && shared_w ? shared_w : nullptr);
+  }
+  const uint16_t* xrow[TT];
+#pragma unroll
+  for (int i = 0; i < TT; ++i) xrow[i] = (t0 + i < T) ? x + (int64_t)(t0 + i) * H : nullptr;
+  float acc[TT][TE];
+#pragma unroll
+  for (int i = 0; i < TT; ++i)
+#pragma unroll
+    for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
+
+  const int nq = H / 8;
+#pragma unroll 4
+  for (int q = lane; q < nq; q += 64) {
+    u32x4 xv[TT], wv[TE];
+#pragma unroll
+    for (int i = 0; i < TT; ++i) xv[i] = xrow[i] ? ld128(xrow[i] + 8 * q) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < TE; ++j) wv[j] = wrow[j] ? ld128(wrow[j] + 8 * q) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int el = 0; el < 8; ++el) {
+      float wf[TE];
+#pragma unroll
+      for (int j = 0; j < TE; ++j)
+        wf[j] = (el & 1) ? bf16hi_to_f32(wv[j][el >> 1]) : bf16lo_to_f32(wv[j][el >> 1]);
+#pragma unroll
+      for (int i = 0; i < TT; ++i) {
+        const uint32_t xd = xv[i][el >> 1];
+        const float xf = (el & 1) ? bf16hi_to_f32(xd) : bf16lo_to_f32(xd);
+#pragma unroll
+        for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xf, wf[j], acc[i][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TT; ++i)
+#pragma unroll
+    for (int j = 0; j < TE; ++j) {
+      float v = acc[i][j];
+      v = wave_xor_sum(v, 32);
+      v = wave_xor_sum(v, 16);
+      v = wave_xor_sum(v, 8);
+      v = wave_xor_sum(v, 4);
+      v = wave_xor_sum(v, 2);
+      v = wave_xor_sum(v, 1);
+      acc[i][j] = v;
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+      for (int j = 0; j < TE; ++j) {
+        const int t = t0 + i, e = e0 + j;
+        if (t < T && e < rows) {
+          float v = acc[i][j];
+          if (bias && e < E) v = v + bias[e];
+          logits[(int64_t)t * (E + 1) + e] = v;
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------- top-k
+// Total order on (logit, expert): larger logit first, then lower id. NaN ranks last.
+MOE_DEV uint64_t topk_key(float v, int e) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if ((__float_as_uint(v) & 0x7FFFFFFFu) > 0x7F800000u) u = 0;
+  return ((uint64_t)u << 32) | (uint32_t)(~(uint32_t)e);
+}
+
+MOE_DEV uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+#define MOE_DPP(v, ctrl, rmask) \
+  (uint32_t) __builtin_amdgcn_update_dpp((int)(v), (int)(v), ctrl, rmask, 0xF, false)
+
+// Wave-wide maximum of a 64-bit key through DPP (quad xor 1, quad xor 2, half-row mirror, row
+// mirror, row_bcast15, row_bcast31); the result is read from lane 63 and is wave-uniform.
+MOE_DEV uint64_t wave_max_u64(uint64_t v) {
+#define MOE_DPP_STEP(ctrl, rmask)                                  \
+  do {                                                             \
+    const uint32_t lo_ = MOE_DPP((uint32_t)v, ctrl, rmask);        \
+    const uint32_t hi_ = MOE_DPP((uint32_t)(v >> 32), ctrl, rmask); \
+    v = max_u64(v, ((uint64_t)hi_ << 32) | lo_);                   \
+  } while (0)
+  MOE_DPP_STEP(0xB1, 0xF);   // quad_perm(1,0,3,2)
+  MOE_DPP_STEP(0x4E, 0xF);   // quad_perm(2,3,0,1)
+  MOE_DPP_STEP(0x141, 0xF);  // row_half_mirror
+  MOE_DPP_STEP(0x140, 0xF);  // row_mirror
+  MOE_DPP_STEP(0x142, 0xA);  // row_bcast15 into rows 1, 3
+  MOE_DPP_STEP(0x143, 0xC);  // row_bcast31 into rows 2, 3
+#undef MOE_DPP_STEP
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// One wave: top-k of row[0..E) (E <= 512). Writes ids[t*k + r], weights[t*k + r] (r < k) and,
+// when has_shared, weights[T*k + t] = sigmoid(row[E]). Optionally mirrors the ids to ids_lds.
+MOE_DEV void topk_token(const float* __restrict__ row, int E, int top_k, int has_shared, int T,
+                        int t, int lane, int32_t* __restrict__ ids, float* __restrict__ weights,
+                        int* ids_lds) {
+  constexpr int MAXC = 8;
+  uint64_t key[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int e = lane + 64 * c;
+    key[c] = e < E ? topk_key(row[e], e) : 0ull;
+  }
+  float my_v = 0.0f;
+  int my_i = 0;
+  for (int r = 0; r < top_k; ++r) {
+    uint64_t head = 0;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) head = max_u64(head, key[c]);
+    const uint64_t best = wave_max_u64(head);
+    const int e = (int)(~(uint32_t)best);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+      if (key[c] == best) key[c] = 0ull;
+    if (lane == r) {
+      my_i = e;
+      my_v = row[e];
+    }
+  }
+  const float vmax = __shfl(my_v, 0, 64);
+  const float ex = (lane < top_k) ? expf(my_v - vmax) : 0.0f;
+  float s = 0.0f;
+  for (int r = 0; r < top_k; ++r) s = s + __shfl(ex, r, 64);
+  if (lane < top_k) {
+    ids[(int64_t)t * top_k + lane] = my_i;
+    weights[(int64_t)t * top_k + lane] = ex / s;
+    if (ids_lds) ids_lds[t * top_k + lane] = my_i;
+  }
+  if (has_shared && lane == 0) {
+    const float g = row[E];
+    weights[(int64_t)T * top_k + t] = 1.0f / (1.0f + expf(-g));
+  }
+}
+
+// ---------------------------------------------------------------------------- align
+constexpr int kAlignWaves = 16;   // align_block needs blockDim.x == 1024
+constexpr int kMaxGroups = 513;   // 512 routed experts + the shared expert
+
+struct AlignSmem {
+  int cnt[kAlignWaves][kMaxGroups];
+  int off[kMaxGroups];
+  int pad[kMaxGroups];
+  int total_padded;
+};
+
+MOE_DEV int slot_expert(const int32_t* topk_ids, int routed, int E, int f) {
+  if (f < routed) {
+    const int e = topk_ids[f];
+    return (e >= 0 && e < E) ? e : -1;
+  }
+  return E;  // shared slot
+}
+
+// topk_ids may point to global memory or LDS (generic address space).
+MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
+                         int cap, int32_t* __restrict__ sorted, int32_t* __restrict__ eids,
+                         int32_t* __restrict__ ntpp, AlignSmem& sm) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int routed = T * top_k;
+  const int n_slots = routed + (has_shared ? T : 0);
+  const int G = E + (has_shared ? 1 : 0);
+  for (int i = tid; i < kAlignWaves * kMaxGroups; i += 1024) (&sm.cnt[0][0])[i] = 0;
+  __syncthreads();
+
+  const int per_wave = (((n_slots + kAlignWaves - 1) / kAlignWaves) + 63) / 64 * 64;
+  const int lo = min(w * per_wave, n_slots), hi = min(lo + per_wave, n_slots);
+  for (int f = lo + lane; f < hi; f += 64) {
+    const int e = slot_expert(topk_ids, routed, E, f);
+    if (e >= 0) atomicAdd(&sm.cnt[w][e], 1);
+  }
+  __syncthreads();
+  for (int g = tid; g < G; g += 1024) {
+    int tot = 0;
+    for (int v = 0; v < kAlignWaves; ++v) tot += sm.cnt[v][g];
+    sm.pad[g] = (tot + BM - 1) / BM * BM;
+  }
+  __syncthreads();
+  if (w == 0) {  // exclusive scan of pad[] by one wave: lane owns a contiguous run
+    const int per = (G + 63) / 64;
+    const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
+    int local = 0;
+    for (int g = g0; g < g1; ++g) local += sm.pad[g];
+    int incl = local;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    int run = incl - local;
+    for (int g = g0; g < g1; ++g) {
+      sm.off[g] = run;
+      run += sm.pad[g];
+    }
+    if (lane == 63) sm.total_padded = incl;
+  }
+  __syncthreads();
+  const int tp = sm.total_padded;
+  for (int g = tid; g < G; g += 1024) {
+    int run = sm.off[g];
+    for (int v = 0; v < kAlignWaves; ++v) {
+      const int c = sm.cnt[v][g];
+      sm.cnt[v][g] = run;
+      run += c;
+    }
+    const int end = sm.off[g] + sm.pad[g];
+    for (int p = run; p < end; ++p)
+      if (p < cap * BM) sorted[p] = n_slots;
+    for (int b = sm.off[g] / BM; b < end / BM; ++b)
+      if (b < cap) eids[b] = g;
+  }
+  for (int b = tp / BM + tid; b < cap; b += 1024) eids[b] = -1;
+  for (int p = tp + tid; p < cap * BM; p += 1024) sorted[p] = n_slots;
+  if (tid == 0) *ntpp = tp;
+  __syncthreads();
+
+  // Stable scatter: ranges in wave order, slots in order inside a range.
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = lo; base < hi; base += 64) {
+    const int f = base + lane;
+    const int e = (f < hi) ? slot_expert(topk_ids, routed, E, f) : -1;
+    const bool valid = e >= 0;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 10; ++bit) {
+      const bool b = valid && ((e >> bit) & 1);
+      const uint64_t bal = __ballot(b);
+      peers &= b ? bal : ~bal;
+    }
+    if (valid) {
+      const int rank = __popcll(peers & lt_mask);
+      const int pos = sm.cnt[w][e] + rank;
+      if (pos < cap * BM) sorted[pos] = f;
+    }
+    // wave-local LDS update after every lane has read the old base
+    __builtin_amdgcn_wave_barrier();
+    if (valid && (__ffsll((long long)peers) - 1) == lane) sm.cnt[w][e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+}

@@ -120,6 +120,28 @@ def test_expert_row_indirection_matches_direct():
         assert torch.equal(a, b)
 
 
+def test_workspace_reusable_across_sizes_and_paths():
+    """One workspace reused by calls of different T and path gives the fresh-workspace result."""
+    _say("workspace reuse")
+    layer = to_gpu(synth.make_layer(6, zipf=True))
+    ws = torch.full((ops.workspace_bytes(2048, 8, layer.experts, False, "prefill") + 4096,), 0x5A,
+                    dtype=torch.uint8, device="cuda")
+    results = {}
+    for T, path in ((1, "decode"), (64, "decode"), (2048, "prefill"), (64, "decode"), (1, "decode"),
+                    (2048, "prefill"), (65, "decode")):
+        x = synth.make_tokens(T, seed=T).cuda()
+        out = ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias,
+                            path=path, workspace=ws)
+        torch.cuda.synchronize()
+        if (T, path) in results:
+            assert torch.equal(results[(T, path)], out), (T, path)
+        else:
+            fresh = ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias,
+                                  path=path)
+            assert torch.equal(fresh, out), (T, path)
+        results[(T, path)] = out
+
+
 def test_layer_is_deterministic():
     _say("determinism")
     layer = to_gpu(synth.make_layer(5, zipf=True))
