@@ -49,6 +49,13 @@ def parse_args() -> argparse.Namespace:
                    help="decode GEMM kernels: MFMA with in-register dequant, or VALU dot2 GEMV")
     p.add_argument("--cpu-baseline-seconds", type=float, default=20.0,
                    help="wall-clock budget of the CPU baseline sample (0 disables it)")
+    p.add_argument("--block-batches", default="1,32",
+                   help="full-block batches (routed experts + gated int4 shared expert); empty disables")
+    p.add_argument("--offload-tokens", type=int, default=512,
+                   help="decode steps of the offloaded-expert run at batch 1 (0 disables it)")
+    p.add_argument("--offload-warmup", type=int, default=16)
+    p.add_argument("--offload-slots", type=int, default=64, help="HBM slots per layer")
+    p.add_argument("--prefetch-k", type=int, default=16, help="predicted experts prefetched per layer")
     p.add_argument("--json-out", default=None, help="also write the full result JSON here")
     return p.parse_args()
 
@@ -242,6 +249,49 @@ def main() -> int:
         log(f"[bench] prefill T={Tp}: {med * 1e3:.1f} us/layer, {prefill['TFLOPs']:.1f} TFLOP/s "
             f"({100 * prefill['mfma_frac']:.1f}% of bf16 MFMA peak)")
 
+    # ------------------------------------------------------- full block with shared expert
+    block = {}
+    block_batches = [int(b) for b in args.block_batches.split(",") if b]
+    if block_batches:
+        from mtp_amd.weights import MoeExperts  # noqa: F401  (shared experts are MoeExperts)
+        shared = [synth.make_experts(1, H, I, seed=4000 + l, device=dev) for l in range(L)]
+        sgate = [synth.make_shared_gate(H, seed=2500 + l, device=dev) for l in range(L)]
+        for T in block_batches:
+            x = synth.make_tokens(T, seed=7, device=dev)
+            need = ops.workspace_bytes(T, K, layers[0].experts, True, "auto")
+            ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+            outs = [torch.empty(T, H, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+            uniq = []
+            for l, ly in enumerate(layers):
+                _, ids, _ = ops.moe_layer(x, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
+                                          shared=shared[l], shared_gate_w=sgate[l], workspace=ws,
+                                          out=outs[l], return_routing=True)
+                uniq.append(int(torch.unique(ids).numel()))
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for l, ly in enumerate(layers):
+                    ops.moe_layer(x, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
+                                  shared=shared[l], shared_gate_w=sgate[l], workspace=ws, out=outs[l])
+            for _ in range(args.warmup):
+                g.replay()
+            ts = median_event_ms(g.replay, args.steps, stream)
+            med = statistics.median(ts)
+            nbytes = (sum(uniq) + L) * per_expert
+            block[str(T)] = {"us_per_layer_p50": med * 1e3 / L, "us_per_layer_p95": pct(ts, 0.95) * 1e3 / L,
+                             "GBps": nbytes / (med * 1e-3) / 1e9,
+                             "U_per_layer_mean": sum(uniq) / L, "shared_experts_per_layer": 1}
+            log(f"[bench] block bs={T}: {block[str(T)]['us_per_layer_p50']:.2f} us/layer "
+                f"{block[str(T)]['GBps']:.0f} GB/s (routed + shared expert bytes)")
+            del g, ws, outs
+        del shared, sgate
+
+    # ------------------------------------------------------------------ offloaded experts
+    offload = None
+    if args.offload_tokens > 0:
+        del graphs, keep, gw1
+        torch.cuda.synchronize()
+        offload = offload_bench(layers, args, dev)
+
     # ------------------------------------------------------------------ CPU baseline
     cpu = None
     if args.cpu_baseline_seconds > 0:
@@ -271,12 +321,104 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode": {str(T): decode[T] for T in batches},
         "prefill": prefill,
+        "block": block,
+        "offload": offload,
     }
     line = json.dumps(result)
     if args.json_out:
         Path(args.json_out).write_text(json.dumps(result, indent=2))
     print(line, flush=True)
     return 0
+
+
+def offload_bench(layers, args, dev) -> dict:
+    """Offloaded experts at batch 1: every (layer, expert) blob in pinned host memory, an HBM pool
+    of `offload_slots` slots per layer, per-layer predictor heads (bf16 2048 -> 1024 SiLU -> 256,
+    random init) reading h = 0.8 x_next + 0.6 eps, top-`prefetch_k` prefetched on the side stream,
+    misses fetched on demand. Three runs over the same token sequence: the random-init predictor,
+    no prefetch (demand only) and a perfect predictor (the next step's true routed experts)."""
+    import torch
+
+    from mtp_amd import ops, synth
+    from mtp_amd.offload import OffloadDecoder, OffloadedExperts
+
+    L, E, H, K = len(layers), synth.NUM_EXPERTS, synth.HIDDEN, synth.TOP_K
+    D = 1024
+    n_tok = args.offload_warmup + args.offload_tokens
+    t0 = time.time()
+    pool = OffloadedExperts(L, E, H, synth.INTERMEDIATE, args.offload_slots, device=dev)
+    for l, ly in enumerate(layers):
+        pool.store_layer(l, ly.experts)
+    torch.cuda.synchronize()
+    log(f"[bench] offload: host pool {pool.host.nbytes / 1e9:.2f} GB pinned, HBM pool "
+        f"{pool.device_pool.numel() / 1e9:.2f} GB, filled in {time.time() - t0:.1f}s")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5000)
+    w1 = (torch.randn(L, D, H, generator=gen, device=dev) / H ** 0.5).to(torch.bfloat16)
+    w2 = (torch.randn(L, E, D, generator=gen, device=dev) / D ** 0.5).to(torch.bfloat16)
+    xs = torch.randn(n_tok + 1, 1, H, generator=gen, device=dev).to(torch.bfloat16)
+    eps = torch.randn(n_tok + 1, 1, H, generator=gen, device=dev)
+    hs = (0.8 * xs.float() + 0.6 * eps).to(torch.bfloat16)
+    routers = [ly.router_w for ly in layers]
+    biases = [ly.logit_bias for ly in layers]
+    # true routed experts of every step (for the perfect-predictor run)
+    true_ids = []
+    for t in range(n_tok + 1):
+        per_layer = []
+        for ly in layers:
+            ids, _, _, _ = ops.router_topk(xs[t], ly.router_w, K, logit_bias=ly.logit_bias)
+            per_layer.append(ids)
+        true_ids.append(torch.stack(per_layer))
+    true_host = torch.stack(true_ids).cpu()
+    true_lists = [[list(dict.fromkeys(true_host[t, l].reshape(-1).tolist())) for l in range(L)]
+                  for t in range(n_tok + 1)]
+
+    runs = {}
+    for name, predictor, k in (("random_predictor", (w1, w2), args.prefetch_k),
+                               ("demand_only", None, 0),
+                               ("perfect_predictor", None, K)):
+        pool.reset_cache()
+        fresh = pool
+        dec = OffloadDecoder(fresh, routers, biases, top_k=K, predictor=predictor, prefetch_k=k,
+                             path=args.decode_path)
+        step_s, base = [], None
+        for t in range(n_tok):
+            if t == args.offload_warmup:
+                torch.cuda.synchronize()
+                base = fresh.stats()
+            t1 = time.perf_counter()
+            if name == "perfect_predictor":
+                pre = true_lists[t + 1]
+            else:
+                pre = dec.predict(hs[t + 1])
+            dec.step(xs[t], pre)
+            torch.cuda.current_stream().synchronize()
+            if t >= args.offload_warmup:
+                step_s.append(time.perf_counter() - t1)
+        torch.cuda.synchronize()
+        st = fresh.stats()
+        diff = {k2: st[k2] - base[k2] for k2 in st if k2 not in ("capacity", "resident_count",
+                                                                  "unused_fetch_count")}
+        diff["unused_fetch_count"] = st["unused_fetch_count"]
+        total = sum(step_s)
+        runs[name] = {
+            "tpot_ms_mean": 1e3 * total / len(step_s),
+            "tpot_ms_p50": 1e3 * statistics.median(step_s),
+            "tpot_ms_p95": 1e3 * pct(step_s, 0.95),
+            "hit_rate": diff["demand_hit_count"] / max(diff["demand_count"], 1),
+            "h2d_GBps": (diff["prefetch_bytes"] + diff["demand_bytes"]) / total / 1e9,
+            "counters": diff,
+        }
+        log(f"[bench] offload {name}: TPOT {runs[name]['tpot_ms_mean']:.2f} ms, hit rate "
+            f"{100 * runs[name]['hit_rate']:.1f}%, H2D {runs[name]['h2d_GBps']:.1f} GB/s")
+    pool.close()
+    del pool
+    return {
+        "workload": f"batch 1, {args.offload_tokens} decode steps after {args.offload_warmup} warmup, "
+                    f"{L} layers x {E} experts in pinned host memory, {args.offload_slots} HBM slots/layer, "
+                    f"prefetch top-{args.prefetch_k} of a random-init bf16 predictor per layer",
+        "runs": runs,
+    }
 
 
 def cpu_baseline(layers, batches, budget_s: float, per_expert: int) -> dict:

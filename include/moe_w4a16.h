@@ -50,8 +50,11 @@ typedef struct moe_gptq_proj_v1 {
 } moe_gptq_proj_v1;
 
 /* A set of int4 experts of one layer: gate/up [E, H/8, I], down [E, I/8, H].
- * expert_row: NULL, or a device int32 [num_experts] map from expert id to the row
- * of the stacked tensors that holds it (an HBM slot pool). */
+ * expert_row: NULL, or a device int32 [num_experts] map from expert id to the row that holds
+ *   it (an HBM slot pool).
+ * expert_stride_bytes: 0 when each of the nine tensors is densely stacked over rows; otherwise
+ *   the byte distance between consecutive rows of every tensor (per-expert blobs of a slot
+ *   pool, with the nine base pointers at the tensors' offsets inside row 0). Multiple of 16. */
 typedef struct moe_expert_set_v1 {
   moe_gptq_proj_v1 gate;
   moe_gptq_proj_v1 up;
@@ -61,6 +64,7 @@ typedef struct moe_expert_set_v1 {
   int32_t hidden;
   int32_t intermediate;
   int32_t group_size;
+  int64_t expert_stride_bytes;
 } moe_expert_set_v1;
 
 /* Kernel path selection for the expert GEMMs (block_m: 16 for DECODE and GEMV, 128 for PREFILL).
@@ -163,6 +167,83 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
                          const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
                          const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
                          uint16_t* out, int32_t path, void* stream);
+
+/* ---------------------------------------------------------------- expert-demand predictor */
+
+/* Workspace bytes of moe_predictor_v1. */
+int64_t moe_predictor_workspace_bytes_v1(int32_t T, int32_t num_heads, int32_t inner,
+                                         int32_t num_experts, int32_t top_k);
+
+/* Top-k experts per layer head predicted from one hidden state by a bf16 MLP per head:
+ * logits[l] = bf16(silu(h . w1[l]^T)) . w2[l]^T in fp32, top-k by (logit desc, id asc).
+ * Replaces the forward of the reference's per-layer predictor
+ * (src/mtp_expert_prefetch/training/hidden_residual.py:44-106), simplified to
+ * hidden -> inner (SiLU) -> num_experts with one weight set per layer. h bf16 [T, hidden];
+ * w1 bf16 [num_heads, inner, hidden]; w2 bf16 [num_heads, num_experts, inner];
+ * topk_ids int32 [num_heads, T, top_k]. */
+int moe_predictor_v1(const uint16_t* h, int32_t T, int32_t hidden, int32_t num_heads,
+                     const uint16_t* w1, int32_t inner, const uint16_t* w2, int32_t num_experts,
+                     int32_t top_k, void* workspace, int64_t workspace_bytes, int32_t* topk_ids,
+                     void* stream);
+
+/* ------------------------------------------------------------------ offloaded slot cache */
+
+/* Expert blobs (expert_bytes each, the nine GPTQ tensors of one expert back to back) for every
+ * (layer, expert) in pinned host memory, and slots_per_layer slots per layer in HBM. The kernels
+ * read a layer's slots through moe_expert_set_v1 with expert_row = device_expert_row + layer *
+ * num_experts and expert_stride_bytes = expert_bytes. dry_run = 1 keeps only the accounting
+ * (no HIP calls; pools may be NULL). */
+typedef struct moe_slot_cache_desc_v1 {
+  int32_t num_layers;
+  int32_t num_experts;
+  int32_t slots_per_layer;
+  int32_t device;
+  int64_t expert_bytes;
+  const void* host_pool;      /* pinned host [num_layers][num_experts][expert_bytes] */
+  void* device_pool;          /* device [num_layers][slots_per_layer][expert_bytes] */
+  int32_t* device_expert_row; /* device [num_layers][num_experts]: expert -> slot */
+  int32_t dry_run;
+  int32_t reserved;
+} moe_slot_cache_desc_v1;
+
+/* Counters with the semantics of ControlledExpertCacheManager
+ * (src/mtp_expert_prefetch/runtime/cache_manager.py:208-279), plus bytes moved. */
+typedef struct moe_slot_cache_counters_v1 {
+  int64_t capacity;
+  int64_t resident_count;
+  int64_t issued_fetch_count;
+  int64_t used_fetch_count;
+  int64_t unused_fetch_count;
+  int64_t demand_count;
+  int64_t demand_hit_count;
+  int64_t demand_miss_count;
+  int64_t evicted_before_use_count;
+  int64_t prefetch_bytes;
+  int64_t demand_bytes;
+} moe_slot_cache_counters_v1;
+
+/* Opaque handle (a magic field is checked on every call). Not thread-safe. */
+int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handle);
+int moe_slot_cache_destroy_v1(uint64_t handle);
+
+/* Prefetch experts (host int32 list) of one layer on the cache's side stream (hipMemcpyAsync),
+ * ordered after every kernel already enqueued on compute_stream. Replaces
+ * ControlledExpertCacheManager.issue_prefetch (cache_manager.py:222-231) with real transfers.
+ * issued: NULL or the number of copies started. */
+int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                               void* compute_stream, int32_t* issued);
+
+/* Make experts of one layer resident before the layer runs on compute_stream: waits for the
+ * layer's prefetches, fetches misses on compute_stream, uploads the expert -> slot table.
+ * Replaces ControlledExpertCacheManager.demand (cache_manager.py:233-247). hits: NULL or the
+ * number of hits. */
+int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                             void* compute_stream, int32_t* hits);
+
+int moe_slot_cache_stats_v1(uint64_t handle, moe_slot_cache_counters_v1* out);
+
+/* Slot of (layer, expert), -1 if absent, -2 for a bad handle or index. */
+int moe_slot_cache_slot_of_v1(uint64_t handle, int32_t layer, int32_t expert);
 
 #ifdef __cplusplus
 }

@@ -43,7 +43,37 @@ EXPORTED = (
     "moe_layer_workspace_bytes_v1",
     "moe_layer_v1",
     "moe_fused_experts_v1",
+    "moe_predictor_workspace_bytes_v1",
+    "moe_predictor_v1",
+    "moe_slot_cache_create_v1",
+    "moe_slot_cache_destroy_v1",
+    "moe_slot_cache_prefetch_v1",
+    "moe_slot_cache_demand_v1",
+    "moe_slot_cache_stats_v1",
+    "moe_slot_cache_slot_of_v1",
 )
+
+
+class SlotCacheDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_layers", c_int32),
+        ("num_experts", c_int32),
+        ("slots_per_layer", c_int32),
+        ("device", c_int32),
+        ("expert_bytes", c_int64),
+        ("host_pool", c_void_p),
+        ("device_pool", c_void_p),
+        ("device_expert_row", c_void_p),
+        ("dry_run", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+class SlotCacheCounters(ctypes.Structure):
+    _fields_ = [(name, c_int64) for name in (
+        "capacity", "resident_count", "issued_fetch_count", "used_fetch_count",
+        "unused_fetch_count", "demand_count", "demand_hit_count", "demand_miss_count",
+        "evicted_before_use_count", "prefetch_bytes", "demand_bytes")]
 
 
 class GptqProj(ctypes.Structure):
@@ -60,6 +90,7 @@ class ExpertSet(ctypes.Structure):
         ("hidden", c_int32),
         ("intermediate", c_int32),
         ("group_size", c_int32),
+        ("expert_stride_bytes", c_int64),
     ]
 
 
@@ -95,6 +126,14 @@ _SIGS = {
     "moe_fused_experts_v1": (
         [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _I, _P],
         c_int32),
+    "moe_predictor_workspace_bytes_v1": ([_I, _I, _I, _I, _I], c_int64),
+    "moe_predictor_v1": ([_P, _I, _I, _I, _P, _I, _P, _I, _I, _P, c_int64, _P, _P], c_int32),
+    "moe_slot_cache_create_v1": ([POINTER(SlotCacheDesc), POINTER(ctypes.c_uint64)], c_int32),
+    "moe_slot_cache_destroy_v1": ([ctypes.c_uint64], c_int32),
+    "moe_slot_cache_prefetch_v1": ([ctypes.c_uint64, _I, _P, _I, _P, POINTER(c_int32)], c_int32),
+    "moe_slot_cache_demand_v1": ([ctypes.c_uint64, _I, _P, _I, _P, POINTER(c_int32)], c_int32),
+    "moe_slot_cache_stats_v1": ([ctypes.c_uint64, POINTER(SlotCacheCounters)], c_int32),
+    "moe_slot_cache_slot_of_v1": ([ctypes.c_uint64, _I, _I], c_int32),
 }
 
 

@@ -8,14 +8,17 @@
 #include "common.h"
 #include "launch.h"
 
-namespace {
+char* moe_error_buffer() {
+  thread_local char buf[kErrorBufferBytes] = "";
+  return buf;
+}
 
-thread_local char g_err[512] = "";
+namespace {
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  vsnprintf(moe_error_buffer(), kErrorBufferBytes, fmt, ap);
   va_end(ap);
   return code;
 }
@@ -50,6 +53,11 @@ int check_experts(const moe_expert_set_v1* ex, const moe_expert_set_v1* sh) {
   if (!(G == 64 || G == 128 || G == 256) || H % G != 0 || I % G != 0)
     return fail(MOE_ERR_SHAPE, "group_size=%d unsupported for hidden=%d intermediate=%d", G, H,
                 I);
+  if (ex->expert_stride_bytes < 0 || ex->expert_stride_bytes % 16 != 0)
+    return fail(MOE_ERR_SHAPE, "expert_stride_bytes=%lld must be a non-negative multiple of 16",
+                (long long)ex->expert_stride_bytes);
+  if (ex->expert_stride_bytes != 0 && !ex->expert_row)
+    return fail(MOE_ERR_NULL, "a strided expert pool needs the expert_row map");
   if (sh) {
     if (!proj_ok(sh->gate) || !proj_ok(sh->up) || !proj_ok(sh->down))
       return fail(MOE_ERR_NULL, "a shared-expert projection pointer is NULL");
@@ -70,6 +78,7 @@ ExpertsDev make_experts_dev(const moe_expert_set_v1* ex, const moe_expert_set_v1
     d.sdown = to_dev(sh->down);
   }
   d.expert_row = ex->expert_row;
+  d.row_stride = ex->expert_stride_bytes;
   d.num_experts = ex->num_experts;
   d.hidden = ex->hidden;
   d.inter = ex->intermediate;
@@ -162,7 +171,45 @@ extern "C" {
 
 int moe_w4a16_abi_version(void) { return MOE_W4A16_ABI_VERSION; }
 
-const char* moe_w4a16_last_error(void) { return g_err; }
+const char* moe_w4a16_last_error(void) { return moe_error_buffer(); }
+
+int64_t moe_predictor_workspace_bytes_v1(int32_t T, int32_t num_heads, int32_t inner,
+                                         int32_t num_experts, int32_t top_k) {
+  if (T < 0 || num_heads < 1 || inner < 1 || num_experts < 1 || top_k < 1) return -1;
+  const size_t L = num_heads;
+  return (int64_t)(align256((size_t)T * (L * inner + 1) * 4) + align256(L * T * inner * 2) +
+                   align256(L * T * (num_experts + 1) * 4) + align256(L * T * top_k * 4));
+}
+
+int moe_predictor_v1(const uint16_t* h, int32_t T, int32_t hidden, int32_t num_heads,
+                     const uint16_t* w1, int32_t inner, const uint16_t* w2, int32_t num_experts,
+                     int32_t top_k, void* workspace, int64_t workspace_bytes, int32_t* topk_ids,
+                     void* stream) {
+  if (T < 0) return fail(MOE_ERR_SHAPE, "predictor: T=%d", T);
+  if (T == 0) return MOE_OK;
+  if (!h || !w1 || !w2 || !workspace || !topk_ids) return fail(MOE_ERR_NULL, "predictor: NULL pointer");
+  if (hidden <= 0 || hidden % 8 != 0 || inner <= 0 || inner % 8 != 0)
+    return fail(MOE_ERR_SHAPE, "predictor: hidden=%d inner=%d must be multiples of 8", hidden, inner);
+  if (num_heads < 1 || num_heads > 1024 || (int64_t)num_heads * inner > (1 << 24))
+    return fail(MOE_ERR_SHAPE, "predictor: num_heads=%d", num_heads);
+  if ((int64_t)T * num_heads > (1 << 24)) return fail(MOE_ERR_SHAPE, "predictor: T * num_heads too large");
+  if (num_experts < 1 || num_experts > 512 || top_k < 1 || top_k > num_experts || top_k > 64)
+    return fail(MOE_ERR_SHAPE, "predictor: num_experts=%d top_k=%d", num_experts, top_k);
+  if (workspace_bytes < moe_predictor_workspace_bytes_v1(T, num_heads, inner, num_experts, top_k))
+    return fail(MOE_ERR_WORKSPACE, "predictor: workspace too small");
+  const size_t L = num_heads;
+  char* ws = static_cast<char*>(workspace);
+  float* z1 = reinterpret_cast<float*>(ws);
+  ws += align256((size_t)T * (L * inner + 1) * 4);
+  uint16_t* a = reinterpret_cast<uint16_t*>(ws);
+  ws += align256(L * T * inner * 2);
+  float* z2 = reinterpret_cast<float*>(ws);
+  ws += align256(L * T * (num_experts + 1) * 4);
+  float* scores = reinterpret_cast<float*>(ws);
+  MOE_CHECK_HIP(launch_predictor(h, T, hidden, num_heads, w1, inner, w2, num_experts, top_k, z1,
+                                 a, z2, topk_ids, scores, (hipStream_t)stream), "predictor");
+  return MOE_OK;
+}
 
 int moe_dequant_v1(const moe_gptq_proj_v1* proj, const int32_t* g_idx, int32_t num_experts,
                    int32_t in_features, int32_t out_features, int32_t group_size,

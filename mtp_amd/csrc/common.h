@@ -76,9 +76,25 @@ struct ExpertsDev {
   ProjDev gate, up, down;
   ProjDev sgate, sup, sdown;     // shared expert (expert id == num_experts), may be null
   const int32_t* expert_row;     // nullable
+  int64_t row_stride;            // bytes between the rows of the routed experts; 0 = dense
   int32_t num_experts;
   int32_t hidden, inter, group;
 };
+
+// Pointers to row `row` of a projection with reduction length K (K8 = K/8 packed rows, NG = K/G
+// groups) and NOUT output columns: densely stacked tensors [rows, ...], or per-expert blobs
+// `stride_bytes` apart (an expert slot pool).
+MOE_DEV ProjDev proj_row(const ProjDev& p, int64_t stride_bytes, int64_t row, int K8, int NG,
+                         int NOUT) {
+  if (stride_bytes) {
+    const int64_t o = row * stride_bytes;
+    return ProjDev{reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(p.qweight) + o),
+                   reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(p.qzeros) + o),
+                   reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.scales) + o)};
+  }
+  return ProjDev{p.qweight + row * K8 * NOUT, p.qzeros + row * NG * (NOUT / 8),
+                 p.scales + row * NG * NOUT};
+}
 
 // A block's expert id is usable: a routed expert, or the shared expert when one is present.
 MOE_DEV bool expert_ok(const ExpertsDev& ed, int e) {

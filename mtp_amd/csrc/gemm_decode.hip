@@ -96,11 +96,13 @@ __global__ __launch_bounds__(512) void gemm_decode_kernel(
     av[s] = valid_m ? ld128(ap + 32 * s) : u32x4{0u, 0u, 0u, 0u};
 
   const int K8 = K / 8, NG = K / G;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) pj[p] = proj_row(pj[p], is_shared ? 0 : ed.row_stride, row, K8, NG, NOUT);
   const int cl = c0 + 2 * (lane & 15);  // this lane's first column
   u32x2 bv[NP][kSteps];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    const int32_t* q = pj[p].qweight + (row * K8 + kw0 / 8 + kq) * NOUT + cl;
+    const int32_t* q = pj[p].qweight + (int64_t)(kw0 / 8 + kq) * NOUT + cl;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s)
       bv[p][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(q + (int64_t)(4 * s) * NOUT));
@@ -114,8 +116,8 @@ __global__ __launch_bounds__(512) void gemm_decode_kernel(
     for (int gi = 0; gi < NGW; ++gi) {
       {
         const int g = kw0 / G + gi;
-        const uint32_t s2 = *reinterpret_cast<const uint32_t*>(pj[p].scales + (row * NG + g) * NOUT + cl);
-        const uint32_t zw = (uint32_t)pj[p].qzeros[(row * NG + g) * (NOUT / 8) + (cl >> 3)] >> (4 * (cl & 7));
+        const uint32_t s2 = *reinterpret_cast<const uint32_t*>(pj[p].scales + (int64_t)g * NOUT + cl);
+        const uint32_t zw = (uint32_t)pj[p].qzeros[(int64_t)g * (NOUT / 8) + (cl >> 3)] >> (4 * (cl & 7));
         sc[p][gi][0] = f16_to_f32(s2 & 0xFFFFu);
         sc[p][gi][1] = f16_to_f32(s2 >> 16);
         zb[p][gi][0] = kMagicBias + (float)(zw & 0xFu);

@@ -115,13 +115,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
     b_col = (tid & 31) * 4;
     b_lds_col = b_col;
   }
-  const int32_t* pq = second ? p1.qweight : p0.qweight;
-  const uint16_t* ps = second ? p1.scales : p0.scales;
-  const int32_t* pz = second ? p1.qzeros : p0.qzeros;
+  const ProjDev pr = proj_row(second ? p1 : p0, is_shared ? 0 : ed.row_stride, row, K8, NG, NOUT);
   const int gcol = n0 + b_col;  // projection column of this thread's first column
-  const int32_t* bq = pq + row * K8 * NOUT + gcol;
-  const uint16_t* bs = ps + row * NG * NOUT + gcol;
-  const int32_t* bz = pz + row * NG * (NOUT / 8) + (gcol >> 3);
+  const int32_t* bq = pr.qweight + gcol;
+  const uint16_t* bs = pr.scales + gcol;
+  const int32_t* bz = pr.qzeros + (gcol >> 3);
   const int zshift = 4 * (gcol & 7);
 
   f32x4 acc[4][4];

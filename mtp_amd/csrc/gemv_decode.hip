@@ -181,15 +181,17 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(const uint16_t* __rest
 
   LaneTile<NP> lt;
 #pragma unroll
+  for (int p = 0; p < NP; ++p) pj[p] = proj_row(pj[p], is_shared ? 0 : ed.row_stride, row, K8, NG, NOUT);
+#pragma unroll
   for (int p = 0; p < NP; ++p) {
-    const int32_t* wq = pj[p].qweight + (row * K8 + ks * kRPK) * NOUT + c;
+    const int32_t* wq = pj[p].qweight + (int64_t)(ks * kRPK) * NOUT + c;
 #pragma unroll
     for (int r = 0; r < kRPK; ++r) lt.w[p][r] = ld128_nt(wq + (int64_t)r * NOUT);
   }
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    const u32x2 s2 = *reinterpret_cast<const u32x2*>(pj[p].scales + (row * NG + g) * NOUT + c);
-    const uint32_t zw = (uint32_t)pj[p].qzeros[(row * NG + g) * (NOUT / 8) + (c >> 3)];
+    const u32x2 s2 = *reinterpret_cast<const u32x2*>(pj[p].scales + (int64_t)g * NOUT + c);
+    const uint32_t zw = (uint32_t)pj[p].qzeros[(int64_t)g * (NOUT / 8) + (c >> 3)];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       lt.s[p][q] = f16_to_f32((s2[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);

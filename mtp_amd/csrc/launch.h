@@ -4,6 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Thread-local message of the last failed entry point (moe_w4a16_last_error).
+constexpr int kErrorBufferBytes = 512;
+char* moe_error_buffer();
+
 struct ProjDev;
 struct ExpertsDev;
 struct SlotsDev;
@@ -55,6 +59,13 @@ hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const Slot
 hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
+
+// Predictor MLP with L heads: z1 = h . w1^T over all L*D rows (fp32 [T][L*D+1]),
+// a = bf16(silu(z1)) head-major [L][T][D], z2[l] = a[l] . w2[l]^T (fp32 [L][T][E+1]),
+// ids/scores [L][T][top_k] = top-k of z2 (scores: renormalised softmax of the top-k).
+hipError_t launch_predictor(const uint16_t* h, int T, int H, int L, const uint16_t* w1, int D,
+                            const uint16_t* w2, int E, int top_k, float* z1, uint16_t* a,
+                            float* z2, int32_t* ids, float* scores, hipStream_t stream);
 
 // Block sizes (slots per block) of the two paths.
 constexpr int kDecodeBlockM = 16;

@@ -1,0 +1,309 @@
+// Offloaded-expert slot cache: pinned host pool of every (layer, expert) blob, an HBM pool of
+// `slots_per_layer` slots per layer, prefetch with hipMemcpyAsync on a private side stream,
+// demand fetch of misses on the compute stream.
+//
+// Accounting follows the reference's ControlledExpertCacheManager
+// (src/mtp_expert_prefetch/runtime/cache_manager.py:208-279): LRU per (layer, expert) with
+// capacity slots_per_layer; a prefetch of a resident key only refreshes its recency; a demand
+// miss inserts the key as used; evicting a prefetched-but-unused entry counts as
+// evicted-before-use. Unlike the reference (accounting only), the bytes really move.
+//
+// Ordering:
+//  * a prefetch first makes the side stream wait for all work enqueued so far on the compute
+//    stream, so a slot is never overwritten while a kernel may still read it;
+//  * a demand makes the compute stream wait for the layer's pending prefetches, fetches its
+//    misses on the compute stream, and uploads the layer's expert->slot table (from a pinned
+//    staging ring) on the compute stream before the layer's kernels.
+// The table entry of an absent expert points at slot 0 (kernels only read rows of routed,
+// demanded experts). Handles are not thread-safe: one handle per host thread.
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include <hip/hip_runtime.h>
+
+#include "launch.h"
+#include "moe_w4a16.h"
+
+namespace {
+
+constexpr uint64_t kMagic = 0x4D4F45534C4F5431ull;  // "MOESLOT1"
+constexpr int kStagingRing = 512;
+
+struct Slot {
+  int expert = -1;
+  bool prefetched = false;
+  bool used = false;
+  uint64_t last_use = 0;
+};
+
+struct Layer {
+  std::vector<Slot> slots;
+  std::vector<int> slot_of;   // expert -> slot or -1
+  bool pending = false;       // prefetch copies not yet waited for by the compute stream
+  hipEvent_t prefetch_done = nullptr;
+};
+
+struct Cache {
+  uint64_t magic = kMagic;
+  moe_slot_cache_desc_v1 d{};
+  std::vector<Layer> layers;
+  uint64_t tick = 0;
+  hipStream_t side = nullptr;
+  hipEvent_t compute_mark = nullptr;
+  int32_t* staging = nullptr;  // pinned [kStagingRing][num_experts]
+  std::vector<hipEvent_t> staging_done;
+  int staging_next = 0;
+  moe_slot_cache_counters_v1 st{};
+};
+
+int fail(int code, const char* msg) {
+  snprintf(moe_error_buffer(), kErrorBufferBytes, "%s", msg);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  snprintf(moe_error_buffer(), kErrorBufferBytes, "%s: HIP error %d (%s)", where, (int)e,
+           hipGetErrorString(e));
+  return MOE_ERR_HIP + ((int)e % 100);
+}
+
+#define SC_HIP(expr, where)                         \
+  do {                                              \
+    hipError_t _e = (expr);                         \
+    if (_e != hipSuccess) return hip_fail(_e, where); \
+  } while (0)
+
+Cache* from_handle(uint64_t h) {
+  Cache* c = reinterpret_cast<Cache*>(h);
+  if (!c || c->magic != kMagic) return nullptr;
+  return c;
+}
+
+bool live(const Cache* c) { return c->d.dry_run == 0; }
+
+const char* host_blob(const Cache* c, int layer, int expert) {
+  return static_cast<const char*>(c->d.host_pool) +
+         ((int64_t)layer * c->d.num_experts + expert) * c->d.expert_bytes;
+}
+
+char* device_slot(const Cache* c, int layer, int slot) {
+  return static_cast<char*>(c->d.device_pool) +
+         ((int64_t)layer * c->d.slots_per_layer + slot) * c->d.expert_bytes;
+}
+
+// Free slot, else the least recently used one. Pure LRU as in the reference: a miss may evict an
+// expert that a later entry of the same demand list names; that entry then misses and is
+// fetched again. With at most slots_per_layer distinct experts per call, every expert of the
+// list is resident when the call returns (the last touches of the call are its experts).
+int pick_slot(const Layer& L) {
+  int best = -1;
+  for (int s = 0; s < (int)L.slots.size(); ++s) {
+    if (L.slots[s].expert < 0) return s;
+    if (best < 0 || L.slots[s].last_use < L.slots[best].last_use) best = s;
+  }
+  return best;
+}
+
+void evict(Cache* c, Layer& L, int s) {
+  Slot& sl = L.slots[s];
+  if (sl.expert >= 0) {
+    if (sl.prefetched && !sl.used) c->st.evicted_before_use_count++;
+    L.slot_of[sl.expert] = -1;
+  }
+  sl = Slot{};
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handle) {
+  if (!desc || !handle) return fail(MOE_ERR_NULL, "slot cache: NULL argument");
+  const moe_slot_cache_desc_v1& d = *desc;
+  if (d.num_layers < 1 || d.num_experts < 1 || d.slots_per_layer < 0 || d.expert_bytes <= 0 ||
+      d.expert_bytes % 16 != 0)
+    return fail(MOE_ERR_SHAPE, "slot cache: bad sizes");
+  if (!d.dry_run && (!d.host_pool || !d.device_pool || !d.device_expert_row))
+    return fail(MOE_ERR_NULL, "slot cache: pools and table are required unless dry_run");
+  Cache* c = new (std::nothrow) Cache();
+  if (!c) return fail(MOE_ERR_SHAPE, "slot cache: out of host memory");
+  c->d = d;
+  c->layers.resize(d.num_layers);
+  for (Layer& L : c->layers) {
+    L.slots.assign(d.slots_per_layer, Slot{});
+    L.slot_of.assign(d.num_experts, -1);
+  }
+  c->st.capacity = d.slots_per_layer;
+  if (live(c)) {
+    SC_HIP(hipSetDevice(d.device), "hipSetDevice");
+    SC_HIP(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking), "create side stream");
+    SC_HIP(hipEventCreateWithFlags(&c->compute_mark, hipEventDisableTiming), "create event");
+    for (Layer& L : c->layers)
+      SC_HIP(hipEventCreateWithFlags(&L.prefetch_done, hipEventDisableTiming), "create event");
+    SC_HIP(hipHostMalloc((void**)&c->staging, (size_t)kStagingRing * d.num_experts * 4,
+                         hipHostMallocDefault), "pinned staging");
+    c->staging_done.assign(kStagingRing, nullptr);
+    for (hipEvent_t& e : c->staging_done)
+      SC_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "create event");
+  }
+  *handle = reinterpret_cast<uint64_t>(c);
+  return MOE_OK;
+}
+
+int moe_slot_cache_destroy_v1(uint64_t handle) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  if (live(c)) {
+    hipSetDevice(c->d.device);
+    hipStreamSynchronize(c->side);
+    for (Layer& L : c->layers) hipEventDestroy(L.prefetch_done);
+    for (hipEvent_t e : c->staging_done) hipEventDestroy(e);
+    hipEventDestroy(c->compute_mark);
+    hipStreamDestroy(c->side);
+    hipHostFree(c->staging);
+  }
+  c->magic = 0;
+  delete c;
+  return MOE_OK;
+}
+
+int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                               void* compute_stream, int32_t* issued) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  if (layer < 0 || layer >= c->d.num_layers || n < 0 || (n > 0 && !experts))
+    return fail(MOE_ERR_SHAPE, "slot cache prefetch: bad layer or list");
+  for (int i = 0; i < n; ++i)
+    if (experts[i] < 0 || experts[i] >= c->d.num_experts)
+      return fail(MOE_ERR_SHAPE, "slot cache: expert id out of range");
+  Layer& L = c->layers[layer];
+  int count = 0;
+  bool ordered = false;
+  for (int i = 0; i < n; ++i) {
+    const int e = experts[i];
+    if (L.slot_of[e] >= 0) {  // resident: refresh recency only
+      L.slots[L.slot_of[e]].last_use = ++c->tick;
+      continue;
+    }
+    c->st.issued_fetch_count++;
+    if (c->d.slots_per_layer == 0) {  // nothing can be kept: counts as evicted before use
+      c->st.evicted_before_use_count++;
+      continue;
+    }
+    const int s = pick_slot(L);
+    evict(c, L, s);
+    L.slots[s] = Slot{e, true, false, ++c->tick};
+    L.slot_of[e] = s;
+    ++count;
+    if (live(c)) {
+      if (!ordered) {  // the side stream runs after every kernel enqueued so far
+        SC_HIP(hipEventRecord(c->compute_mark, (hipStream_t)compute_stream), "record compute mark");
+        SC_HIP(hipStreamWaitEvent(c->side, c->compute_mark, 0), "side waits compute");
+        ordered = true;
+      }
+      SC_HIP(hipMemcpyAsync(device_slot(c, layer, s), host_blob(c, layer, e), c->d.expert_bytes,
+                            hipMemcpyHostToDevice, c->side), "prefetch copy");
+      c->st.prefetch_bytes += c->d.expert_bytes;
+    }
+  }
+  if (count > 0 && live(c)) {
+    SC_HIP(hipEventRecord(L.prefetch_done, c->side), "record prefetch done");
+    L.pending = true;
+  }
+  if (issued) *issued = count;
+  return MOE_OK;
+}
+
+int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                             void* compute_stream, int32_t* hits) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  if (layer < 0 || layer >= c->d.num_layers || n < 0 || (n > 0 && !experts))
+    return fail(MOE_ERR_SHAPE, "slot cache demand: bad layer or list");
+  Layer& L = c->layers[layer];
+  {  // validate ids and count distinct experts before any state changes
+    std::vector<char> seen(c->d.num_experts, 0);
+    int distinct = 0;
+    for (int i = 0; i < n; ++i) {
+      const int e = experts[i];
+      if (e < 0 || e >= c->d.num_experts)
+        return fail(MOE_ERR_SHAPE, "slot cache: expert id out of range");
+      distinct += seen[e] ? 0 : 1;
+      seen[e] = 1;
+    }
+    if (distinct > c->d.slots_per_layer && live(c))
+      return fail(MOE_ERR_SHAPE, "slot cache demand: more distinct experts than slots");
+  }
+  hipStream_t cs = (hipStream_t)compute_stream;
+  if (L.pending && live(c)) {
+    SC_HIP(hipStreamWaitEvent(cs, L.prefetch_done, 0), "compute waits prefetch");
+    L.pending = false;
+  }
+  int nh = 0;
+  for (int i = 0; i < n; ++i) {
+    const int e = experts[i];
+    c->st.demand_count++;
+    int s = L.slot_of[e];
+    if (s >= 0) {
+      c->st.demand_hit_count++;
+      ++nh;
+      Slot& sl = L.slots[s];
+      if (sl.prefetched && !sl.used) c->st.used_fetch_count++;
+      sl.used = true;
+      sl.last_use = ++c->tick;
+      continue;
+    }
+    c->st.demand_miss_count++;
+    if (c->d.slots_per_layer == 0) continue;
+    s = pick_slot(L);
+    evict(c, L, s);
+    L.slots[s] = Slot{e, false, true, ++c->tick};
+    L.slot_of[e] = s;
+    if (live(c)) {
+      SC_HIP(hipMemcpyAsync(device_slot(c, layer, s), host_blob(c, layer, e), c->d.expert_bytes,
+                            hipMemcpyHostToDevice, cs), "demand copy");
+      c->st.demand_bytes += c->d.expert_bytes;
+    }
+  }
+  if (live(c)) {  // publish the layer's expert -> slot table on the compute stream
+    const int r = c->staging_next;
+    c->staging_next = (r + 1) % kStagingRing;
+    SC_HIP(hipEventSynchronize(c->staging_done[r]), "staging reuse");
+    int32_t* stage = c->staging + (size_t)r * c->d.num_experts;
+    for (int e = 0; e < c->d.num_experts; ++e) stage[e] = L.slot_of[e] >= 0 ? L.slot_of[e] : 0;
+    SC_HIP(hipMemcpyAsync(c->d.device_expert_row + (size_t)layer * c->d.num_experts, stage,
+                          (size_t)c->d.num_experts * 4, hipMemcpyHostToDevice, cs), "table upload");
+    SC_HIP(hipEventRecord(c->staging_done[r], cs), "record staging");
+  }
+  if (hits) *hits = nh;
+  return MOE_OK;
+}
+
+int moe_slot_cache_stats_v1(uint64_t handle, moe_slot_cache_counters_v1* out) {
+  Cache* c = from_handle(handle);
+  if (!c || !out) return fail(MOE_ERR_NULL, "slot cache: bad handle or NULL output");
+  moe_slot_cache_counters_v1 s = c->st;
+  int64_t resident = 0, unused = 0;
+  for (const Layer& L : c->layers)
+    for (const Slot& sl : L.slots)
+      if (sl.expert >= 0) {
+        ++resident;
+        if (sl.prefetched && !sl.used) ++unused;
+      }
+  s.resident_count = resident;
+  s.unused_fetch_count = unused;
+  *out = s;
+  return MOE_OK;
+}
+
+int moe_slot_cache_slot_of_v1(uint64_t handle, int32_t layer, int32_t expert) {
+  Cache* c = from_handle(handle);
+  if (!c || layer < 0 || layer >= c->d.num_layers || expert < 0 || expert >= c->d.num_experts)
+    return -2;
+  return c->layers[layer].slot_of[expert];
+}
+
+}  // extern "C"

@@ -1,0 +1,352 @@
+"""Offloaded experts: every (layer, expert) blob in pinned host memory, an HBM slot pool per layer,
+prefetch on a side stream driven by a predictor, demand fetch of misses on the compute stream.
+
+Reference behaviour this replaces:
+  * cache accounting  src/mtp_expert_prefetch/runtime/cache_manager.py:208-279
+    (ControlledExpertCacheManager: LRU per (layer, expert), counters issued / used / unused /
+    evicted-before-use / demand hit / miss). Here the capacity is per layer (the slots of that
+    layer's HBM pool) and the bytes really move (hipMemcpyAsync H2D).
+  * predictor         src/mtp_expert_prefetch/training/hidden_residual.py:44-106, simplified to
+    one bf16 MLP head per layer (hidden -> inner SiLU -> experts) whose top-k is prefetched.
+
+Expert blob: the nine GPTQ tensors of one expert back to back (no g_idx; the kernels assume
+g_idx[k] = k // group_size), in the order gate, up, down and qweight, qzeros, scales inside each
+projection. At the Qwen3-MoE shape (H 2048, I 512, G 128) the blob is 1 634 304 bytes. The
+kernels read a layer's slots through an ExpertSet whose tensors point into slot 0 of that layer
+with expert_stride_bytes = blob size and expert_row = the layer's expert -> slot table.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from mtp_amd import _lib, ops
+from mtp_amd.weights import GptqStack, MoeExperts
+
+PIECES = ("qweight", "qzeros", "scales")
+PROJ_ORDER = ("gate", "up", "down")
+
+
+@dataclass(frozen=True)
+class BlobPiece:
+    proj: str
+    kind: str
+    offset: int
+    shape: tuple[int, int]
+    dtype: torch.dtype
+
+    @property
+    def nbytes(self) -> int:
+        return self.shape[0] * self.shape[1] * torch.empty((), dtype=self.dtype).element_size()
+
+
+def blob_layout(hidden: int, inter: int, group_size: int) -> tuple[list[BlobPiece], int]:
+    """Pieces of one expert blob (offsets in bytes) and the blob size."""
+    pieces: list[BlobPiece] = []
+    off = 0
+    for proj, (k, n) in zip(PROJ_ORDER, ((hidden, inter), (hidden, inter), (inter, hidden))):
+        if k % group_size or k % 8 or n % 8:
+            raise ValueError(f"{proj}: in={k} out={n} group={group_size} do not tile")
+        for kind, shape, dtype in (("qweight", (k // 8, n), torch.int32),
+                                   ("qzeros", (k // group_size, n // 8), torch.int32),
+                                   ("scales", (k // group_size, n), torch.float16)):
+            piece = BlobPiece(proj, kind, off, shape, dtype)
+            if off % 16:
+                raise ValueError("blob pieces must stay 16-byte aligned")
+            pieces.append(piece)
+            off += piece.nbytes
+    if off % 16:
+        raise ValueError("blob size must be a multiple of 16 bytes")
+    return pieces, off
+
+
+def pack_blobs(experts: MoeExperts) -> torch.Tensor:
+    """uint8 [num_experts, blob] of a resident (contiguous) expert set, on its device."""
+    experts.validate()
+    pieces, _ = blob_layout(experts.hidden_size, experts.intermediate_size, experts.group_size)
+    stacks = {"gate": experts.gate, "up": experts.up, "down": experts.down}
+    parts = []
+    for p in pieces:
+        t = getattr(stacks[p.proj], p.kind)
+        parts.append(t.reshape(t.shape[0], -1).view(torch.uint8))
+    return torch.cat(parts, dim=1)
+
+
+# ----------------------------------------------------------------------------- pinned host memory
+class PinnedHostBuffer:
+    """hipHostMalloc'd host memory (page-locked, so hipMemcpyAsync from it is a true async DMA).
+
+    Allocated through the HIP runtime that torch has already loaded (one runtime per process).
+    """
+
+    def __init__(self, nbytes: int) -> None:
+        if nbytes <= 0:
+            raise ValueError("nbytes must be positive")
+        torch.cuda.init()
+        self._hip = ctypes.CDLL("libamdhip64.so.7")
+        self._hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t,
+                                            ctypes.c_uint]
+        self._hip.hipHostMalloc.restype = ctypes.c_int
+        self._hip.hipHostFree.argtypes = [ctypes.c_void_p]
+        self._hip.hipHostFree.restype = ctypes.c_int
+        ptr = ctypes.c_void_p()
+        err = self._hip.hipHostMalloc(ctypes.byref(ptr), ctypes.c_size_t(nbytes), 0)
+        if err != 0 or not ptr.value:
+            raise MemoryError(f"hipHostMalloc({nbytes}) failed with HIP error {err}")
+        self.ptr = int(ptr.value)
+        self.nbytes = int(nbytes)
+
+    def view(self) -> torch.Tensor:
+        """A CPU uint8 tensor over the buffer (valid while the buffer is open)."""
+        if not self.ptr:
+            raise RuntimeError("buffer is closed")
+        arr = (ctypes.c_uint8 * self.nbytes).from_address(self.ptr)
+        return torch.frombuffer(arr, dtype=torch.uint8)
+
+    def close(self) -> None:
+        if self.ptr:
+            self._hip.hipHostFree(ctypes.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter teardown order varies
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ----------------------------------------------------------------------------- slot cache
+class SlotCache:
+    """ctypes handle of moe_slot_cache_*_v1. dry_run=True keeps only the accounting."""
+
+    def __init__(self, num_layers: int, num_experts: int, slots_per_layer: int, expert_bytes: int,
+                 *, host_pool: int = 0, device_pool: int = 0, expert_row: int = 0,
+                 device: int = 0, dry_run: bool = False) -> None:
+        self._lib = _lib.load()
+        desc = _lib.SlotCacheDesc(num_layers, num_experts, slots_per_layer, device, expert_bytes,
+                                  host_pool, device_pool, expert_row, int(dry_run), 0)
+        handle = ctypes.c_uint64()
+        _lib.check(self._lib.moe_slot_cache_create_v1(ctypes.byref(desc), ctypes.byref(handle)))
+        self.handle = handle.value
+        self.num_layers = num_layers
+        self.num_experts = num_experts
+        self.dry_run = dry_run
+
+    @staticmethod
+    def _ids(experts) -> tuple[ctypes.Array, int]:
+        vals = [int(e) for e in experts]
+        return (ctypes.c_int32 * max(len(vals), 1))(*vals), len(vals)
+
+    def _stream(self, stream) -> int | None:
+        if self.dry_run:
+            return None
+        s = stream if stream is not None else torch.cuda.current_stream()
+        return s.cuda_stream
+
+    def prefetch(self, layer: int, experts, stream=None) -> int:
+        """Start copies of the non-resident experts on the side stream; returns copies started."""
+        arr, n = self._ids(experts)
+        issued = ctypes.c_int32()
+        _lib.check(self._lib.moe_slot_cache_prefetch_v1(self.handle, layer, arr, n,
+                                                        self._stream(stream), ctypes.byref(issued)))
+        return issued.value
+
+    def demand(self, layer: int, experts, stream=None) -> int:
+        """Make the experts resident before the next work on `stream`; returns hits."""
+        arr, n = self._ids(experts)
+        hits = ctypes.c_int32()
+        _lib.check(self._lib.moe_slot_cache_demand_v1(self.handle, layer, arr, n,
+                                                      self._stream(stream), ctypes.byref(hits)))
+        return hits.value
+
+    def stats(self) -> dict[str, int]:
+        c = _lib.SlotCacheCounters()
+        _lib.check(self._lib.moe_slot_cache_stats_v1(self.handle, ctypes.byref(c)))
+        return {name: int(getattr(c, name)) for name, _ in _lib.SlotCacheCounters._fields_}
+
+    def slot_of(self, layer: int, expert: int) -> int:
+        s = int(self._lib.moe_slot_cache_slot_of_v1(self.handle, layer, expert))
+        if s == -2:
+            raise IndexError(f"(layer {layer}, expert {expert}) out of range")
+        return s
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.check(self._lib.moe_slot_cache_destroy_v1(self.handle))
+            self.handle = 0
+
+    def __enter__(self) -> "SlotCache":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+
+# ----------------------------------------------------------------------------- offloaded layers
+class OffloadedExperts:
+    """Host pool of [num_layers][num_experts] blobs, HBM pool of [num_layers][slots] blobs, and
+    the slot cache that moves blobs between them.
+
+    Fill the host pool with `store_layer`, then per layer: `demand` the routed experts, run the
+    kernels on `layer_experts(layer)`, and `prefetch` predicted experts of later steps.
+    """
+
+    def __init__(self, num_layers: int, num_experts: int, hidden: int, inter: int,
+                 slots_per_layer: int, *, group_size: int = 128, device=None) -> None:
+        self.device = torch.device(device if device is not None else "cuda")
+        if self.device.type != "cuda":
+            raise ValueError("offloaded experts need a ROCm device")
+        self.num_layers, self.num_experts = num_layers, num_experts
+        self.hidden, self.inter, self.group_size = hidden, inter, group_size
+        self.slots = slots_per_layer
+        self.pieces, self.blob = blob_layout(hidden, inter, group_size)
+        self.host = PinnedHostBuffer(num_layers * num_experts * self.blob)
+        self.device_pool = torch.empty(num_layers, max(slots_per_layer, 1), self.blob,
+                                       dtype=torch.uint8, device=self.device)
+        self.expert_row = torch.zeros(num_layers, num_experts, dtype=torch.int32,
+                                      device=self.device)
+        self.cache = SlotCache(num_layers, num_experts, slots_per_layer, self.blob,
+                               host_pool=self.host.ptr, device_pool=self.device_pool.data_ptr(),
+                               expert_row=self.expert_row.data_ptr(),
+                               device=self.device.index or 0)
+        self._views = [self._layer_view(l) for l in range(num_layers)]
+
+    def _layer_view(self, layer: int) -> MoeExperts:
+        base = self.device_pool[layer]  # [slots, blob] uint8
+        stacks = {}
+        for proj in PROJ_ORDER:
+            parts = {}
+            for p in self.pieces:
+                if p.proj != proj:
+                    continue
+                width = p.nbytes // torch.empty((), dtype=p.dtype).element_size()
+                v = base[:, p.offset:p.offset + p.nbytes].view(p.dtype)  # [slots, width]
+                parts[p.kind] = v.as_strided((v.shape[0],) + p.shape, (v.stride(0), p.shape[1], 1))
+                assert width == p.shape[0] * p.shape[1]
+            stacks[proj] = GptqStack(parts["qweight"], parts["qzeros"], parts["scales"])
+        return MoeExperts(stacks["gate"], stacks["up"], stacks["down"], self.group_size,
+                          expert_row=self.expert_row[layer], num_experts=self.num_experts,
+                          expert_stride_bytes=self.blob)
+
+    def reset_cache(self) -> None:
+        """Forget every resident slot and counter (pools are kept; the next demands refetch)."""
+        torch.cuda.synchronize(self.device)
+        self.cache.close()
+        self.cache = SlotCache(self.num_layers, self.num_experts, self.slots, self.blob,
+                               host_pool=self.host.ptr, device_pool=self.device_pool.data_ptr(),
+                               expert_row=self.expert_row.data_ptr(),
+                               device=self.device.index or 0)
+
+    def layer_experts(self, layer: int) -> MoeExperts:
+        """Expert set of one layer reading its HBM slots (valid after `demand`)."""
+        return self._views[layer]
+
+    def store_layer(self, layer: int, experts: MoeExperts) -> None:
+        """Copy a resident layer's experts into the host pool (blob layout)."""
+        if (experts.hidden_size, experts.intermediate_size, experts.group_size) != (
+                self.hidden, self.inter, self.group_size):
+            raise ValueError("expert shapes do not match the pool")
+        if experts.gate.num_rows != self.num_experts or experts.expert_row is not None:
+            raise ValueError("store_layer needs a dense stack of all num_experts experts")
+        blobs = pack_blobs(experts)
+        n = self.num_experts * self.blob
+        dst = self.host.view()[layer * n:(layer + 1) * n]
+        dst.copy_(blobs.reshape(-1))  # device -> pinned host DMA when the stack is on the GPU
+        del blobs
+
+    def prefetch(self, layer: int, experts, stream=None) -> int:
+        return self.cache.prefetch(layer, experts, stream)
+
+    def demand(self, layer: int, experts, stream=None) -> int:
+        return self.cache.demand(layer, experts, stream)
+
+    def stats(self) -> dict[str, int]:
+        return self.cache.stats()
+
+    def close(self) -> None:
+        torch.cuda.synchronize(self.device)
+        self.cache.close()
+        self.host.close()
+
+
+def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts, layer: int, *,
+                 top_k: int = 8, logit_bias: torch.Tensor | None = None,
+                 ids_host: torch.Tensor | None = None, path: str = "auto",
+                 workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One offloaded MoE layer: router -> ids to the host -> demand -> experts from the slots.
+
+    The host wait for the routed ids is the one synchronisation per layer that a host-managed
+    cache needs (the reference's demand() is a host call on the routed ids too,
+    cache_manager.py:233-247). Returns (out bf16 [T, H], routed ids on the host int32 [T, k]).
+    """
+    ids, w, _, _ = ops.router_topk(x, router_w, top_k, logit_bias=logit_bias)
+    if ids_host is None or ids_host.shape != ids.shape:
+        ids_host = torch.empty(ids.shape, dtype=torch.int32, pin_memory=True)
+    ids_host.copy_(ids, non_blocking=True)
+    torch.cuda.current_stream().synchronize()
+    pool.demand(layer, ids_host.reshape(-1).tolist())
+    out = ops.fused_experts(x, ids, w, pool.layer_experts(layer), path=path, workspace=workspace)
+    return out, ids_host
+
+
+class OffloadDecoder:
+    """Decode steps through offloaded MoE layers, with prefetch of predicted experts.
+
+    Per layer: router -> routed ids to the host -> demand (misses copied on the compute stream)
+    -> experts from the layer's slots -> prefetch of the experts predicted for the next step
+    (side stream, ordered after this layer's kernels so a slot is never overwritten while read).
+    Each layer reads the step's hidden state x (independent synthetic layers).
+    """
+
+    def __init__(self, pool: OffloadedExperts, routers: list[torch.Tensor],
+                 biases: list[torch.Tensor | None], *, top_k: int = 8,
+                 predictor: tuple[torch.Tensor, torch.Tensor] | None = None,
+                 prefetch_k: int = 16, path: str = "auto") -> None:
+        if len(routers) != pool.num_layers or len(biases) != pool.num_layers:
+            raise ValueError("one router weight and bias per layer")
+        self.pool, self.routers, self.biases = pool, routers, biases
+        self.top_k, self.path, self.prefetch_k = top_k, path, prefetch_k
+        self.predictor = predictor
+        if predictor is not None:
+            w1, w2 = predictor
+            if w1.shape[0] != pool.num_layers or w2.shape[0] != pool.num_layers:
+                raise ValueError("predictor needs one head per layer")
+        self._ids_host: torch.Tensor | None = None
+        self._pred_host: torch.Tensor | None = None
+        self._ws: torch.Tensor | None = None
+        self._pred_ws: torch.Tensor | None = None
+
+    def predict(self, h: torch.Tensor) -> list[list[int]]:
+        """Per layer, the distinct experts of the predictor's top-prefetch_k over h's rows."""
+        if self.predictor is None or self.prefetch_k <= 0:
+            return [[] for _ in range(self.pool.num_layers)]
+        w1, w2 = self.predictor
+        L, T, k = self.pool.num_layers, h.shape[0], self.prefetch_k
+        need = ops.predictor_workspace_bytes(T, L, w1.shape[1], w2.shape[1], k)
+        if self._pred_ws is None or self._pred_ws.numel() < need:
+            self._pred_ws = torch.empty(need, dtype=torch.uint8, device=h.device)
+        ids = ops.predictor_topk(h, w1, w2, k, workspace=self._pred_ws)
+        if self._pred_host is None or self._pred_host.shape != ids.shape:
+            self._pred_host = torch.empty(ids.shape, dtype=torch.int32, pin_memory=True)
+        self._pred_host.copy_(ids, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        return [list(dict.fromkeys(self._pred_host[l].reshape(-1).tolist())) for l in range(L)]
+
+    def step(self, x: torch.Tensor, prefetch: list[list[int]] | None = None) -> list[torch.Tensor]:
+        """One decode step over every layer; `prefetch[l]` is issued right after layer l."""
+        T = x.shape[0]
+        need = ops.workspace_bytes(T, self.top_k, self.pool.layer_experts(0), False, self.path)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+        outs = []
+        for l in range(self.pool.num_layers):
+            out, self._ids_host = routed_layer(x, self.routers[l], self.pool, l, top_k=self.top_k,
+                                               logit_bias=self.biases[l], ids_host=self._ids_host,
+                                               path=self.path, workspace=self._ws)
+            if prefetch is not None and prefetch[l]:
+                self.pool.prefetch(l, prefetch[l])
+            outs.append(out)
+        return outs

@@ -44,6 +44,14 @@ def _require_gpu(*tensors: torch.Tensor | None) -> None:
             raise ValueError(f"tensors on different devices: {dev} and {t.device}")
 
 
+def _require_experts_on(device: torch.device, *sets: MoeExperts | None) -> None:
+    """Expert sets are validated by MoeExperts.validate (contiguous stacks or slot-pool views);
+    here only their device is checked against the activations'."""
+    for ex in sets:
+        if ex is not None and ex.device != device:
+            raise ValueError(f"expert weights on {ex.device}, activations on {device}")
+
+
 def _path(path: str | int) -> int:
     if isinstance(path, int):
         return path
@@ -221,7 +229,8 @@ def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, t
         raise ValueError(f"router_w has {router_w.shape[0]} rows for {experts.num_experts} experts")
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w must be given together")
-    _require_gpu(x, router_w, logit_bias, shared_gate_w, experts.gate.qweight)
+    _require_gpu(x, router_w, logit_bias, shared_gate_w)
+    _require_experts_on(x.device, experts, shared)
     T = x.shape[0]
     p = _path(path)
     need = workspace_bytes(T, top_k, experts, shared is not None, p)
@@ -257,7 +266,8 @@ def fused_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.T
         raise ValueError("topk_ids/topk_weights must be [T, k] matching the input rows")
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w must be given together")
-    _require_gpu(x, topk_ids, topk_weights, shared_gate_w, experts.gate.qweight)
+    _require_gpu(x, topk_ids, topk_weights, shared_gate_w)
+    _require_experts_on(x.device, experts, shared)
     T, k = topk_ids.shape
     p = _path(path)
     need = workspace_bytes(T, k, experts, shared is not None, p)
@@ -270,4 +280,50 @@ def fused_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.T
         x.data_ptr(), T, topk_ids.data_ptr(), topk_weights.data_ptr(), k, ctypes.byref(ex),
         ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
         workspace.numel(), out.data_ptr(), p, _stream()))
+    return out
+
+
+# ----------------------------------------------------------------------------- predictor
+def predictor_workspace_bytes(T: int, num_heads: int, inner: int, num_experts: int, top_k: int) -> int:
+    return int(_lib.load().moe_predictor_workspace_bytes_v1(T, num_heads, inner, num_experts, top_k))
+
+
+def predictor_topk(h: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, top_k: int = 16, *,
+                   workspace: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-layer predicted experts: int32 [L, T, top_k] from h bf16 [T, H], w1 bf16 [L, D, H]
+    (or [D, H] for one head), w2 bf16 [L, E, D] (or [E, D]).
+
+    Each head computes bf16(silu(h . w1[l]^T)) . w2[l]^T in fp32 and keeps its top-k by
+    (logit desc, id asc); the reference's per-layer predictor head
+    (src/mtp_expert_prefetch/training/hidden_residual.py:44-106) simplified to hidden -> inner
+    (SiLU) -> experts.
+    """
+    lib = _lib.load()
+    if w1.dim() == 2:
+        w1 = w1.unsqueeze(0)
+    if w2.dim() == 2:
+        w2 = w2.unsqueeze(0)
+    _bf16_matrix(h, "hidden")
+    if w1.dim() != 3 or w2.dim() != 3 or w1.shape[0] != w2.shape[0]:
+        raise ValueError("w1 must be [L, D, H] and w2 [L, E, D] with the same L")
+    L, D, H = w1.shape
+    E = w2.shape[1]
+    if H != h.shape[1] or w2.shape[2] != D:
+        raise ValueError(f"predictor shapes: h {tuple(h.shape)}, w1 {tuple(w1.shape)}, w2 {tuple(w2.shape)}")
+    for t, name in ((w1, "w1"), (w2, "w2")):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise TypeError(f"{name} must be contiguous bf16")
+    _require_gpu(h, w1, w2)
+    T = h.shape[0]
+    need = predictor_workspace_bytes(T, L, D, E, top_k)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=h.device)
+    if out is None:
+        out = torch.empty(L, T, top_k, dtype=torch.int32, device=h.device)
+    elif out.dtype != torch.int32 or out.shape != (L, T, top_k) or not out.is_contiguous():
+        raise ValueError("out must be contiguous int32 [L, T, top_k]")
+    _lib.check(lib.moe_predictor_v1(h.data_ptr(), T, H, L, w1.data_ptr(), D, w2.data_ptr(), E,
+                                    top_k, workspace.data_ptr(), workspace.numel(),
+                                    out.data_ptr(), _stream()))
     return out

@@ -39,14 +39,19 @@ class GptqStack:
     def out_features(self) -> int:
         return int(self.qweight.shape[2])
 
-    def validate(self, group_size: int) -> None:
+    def validate(self, group_size: int, row_stride_bytes: int = 0) -> None:
+        """Check dtypes and shapes. row_stride_bytes > 0: the rows are blobs of a slot pool, so
+        each tensor's rows are contiguous and row r starts row_stride_bytes after row r - 1."""
         for name in ("qweight", "qzeros", "scales"):
             t = getattr(self, name)
             if not isinstance(t, torch.Tensor):
                 raise TypeError(f"{name} must be a torch.Tensor")
             if t.ndim != 3:
                 raise ValueError(f"{name} must be 3D [E, ...], got {tuple(t.shape)}")
-            if not t.is_contiguous():
+            if row_stride_bytes:
+                if not t[0].is_contiguous() or t.stride(0) * t.element_size() != row_stride_bytes:
+                    raise ValueError(f"{name} rows must be contiguous and {row_stride_bytes} B apart")
+            elif not t.is_contiguous():
                 raise ValueError(f"{name} must be contiguous")
         if self.qweight.dtype != torch.int32 or self.qzeros.dtype != torch.int32:
             raise TypeError("qweight and qzeros must be int32")
@@ -87,6 +92,7 @@ class MoeExperts:
     group_size: int = 128
     expert_row: torch.Tensor | None = None  # int32 [num_experts] rows of the stacks
     num_experts: int | None = None           # logical expert count (defaults to stack rows)
+    expert_stride_bytes: int = 0             # > 0: rows are blobs of a slot pool, this far apart
 
     def __post_init__(self) -> None:
         if self.num_experts is None:
@@ -110,7 +116,9 @@ class MoeExperts:
         if self._validated:
             return
         for p in (self.gate, self.up, self.down):
-            p.validate(self.group_size)
+            p.validate(self.group_size, self.expert_stride_bytes)
+        if self.expert_stride_bytes and self.expert_row is None:
+            raise ValueError("a slot pool (expert_stride_bytes > 0) needs expert_row")
         h, i = self.hidden_size, self.intermediate_size
         if self.up.in_features != h or self.up.out_features != i:
             raise ValueError("gate_proj and up_proj shapes must match")
@@ -126,7 +134,8 @@ class MoeExperts:
         return _lib.ExpertSet(
             self.gate.struct(), self.up.struct(), self.down.struct(),
             0 if self.expert_row is None else self.expert_row.data_ptr(),
-            int(self.num_experts), self.hidden_size, self.intermediate_size, int(self.group_size))
+            int(self.num_experts), self.hidden_size, self.intermediate_size, int(self.group_size),
+            int(self.expert_stride_bytes))
 
     def nbytes_per_expert(self) -> int:
         """Packed qweight + fp16 scales + packed qzeros of one expert (g_idx excluded)."""

@@ -260,3 +260,23 @@ def moe_tokens_bf16(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
         sg = torch.sigmoid(F.linear(flat_x, shared_gate_w))
         output = output + sg * F.linear(F.silu(F.linear(flat_x, wg)) * F.linear(flat_x, wu), wd)
     return output.reshape_as(x)
+
+
+# --------------------------------------------------------------------------- predictor
+def predictor_ref(h_bits: np.ndarray, w1_bits: np.ndarray, w2_bits: np.ndarray, top_k: int):
+    """Per-layer predictor heads (training/hidden_residual.py:44-106, simplified to
+    hidden -> inner SiLU -> experts): z1 = h . w1[l]^T (canonical fp32 order),
+    a = bf16_RNE(z1 / (1 + exp(-z1))) in fp32, logits = a . w2[l]^T (canonical order),
+    ids = stable top-k. h_bits [T, H]; w1_bits [L, D, H]; w2_bits [L, E, D].
+    Returns (ids int32 [L, T, k], logits fp32 [L, T, E])."""
+    h = gptq_ref.bf16_bits_to_f32(h_bits)
+    L = w1_bits.shape[0]
+    ids, logits = [], []
+    for l in range(L):
+        z1 = canonical_dot_rows(h, gptq_ref.bf16_bits_to_f32(w1_bits[l]))
+        act = (z1 / (np.float32(1.0) + np.exp(-z1))).astype(np.float32)
+        a = gptq_ref.bf16_bits_to_f32(gptq_ref.f32_to_bf16_bits(act))
+        z2 = canonical_dot_rows(a, gptq_ref.bf16_bits_to_f32(w2_bits[l]))
+        logits.append(z2)
+        ids.append(stable_topk(z2, top_k))
+    return np.stack(ids), np.stack(logits)

@@ -1,0 +1,120 @@
+"""GPU tests of the offloaded-expert path: slot cache with real copies, slot-pool expert sets,
+and the per-layer predictor.
+
+* A layer read from its HBM slots must give bit-identical output to the same layer read from a
+  resident stack (same kernels, same bytes), for every path, after evictions and prefetches.
+* Slot contents must equal the host blob of the expert the table names (byte-exact).
+* The predictor's top-k must match the oracle's (predictor_ref); a position may differ only
+  where the oracle's logits of the two experts involved are within 1e-4 relative of each other
+  (a one-ulp difference of expf in SiLU can move one bf16 activation by one step).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mtp_amd import ops, synth
+from mtp_amd.offload import OffloadedExperts, pack_blobs, routed_layer
+from oracle import moe_ref
+from tests.helpers import LAYER_RTOL, bf16_bits, experts_to_np, small_layer, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def pooled():
+    _say("offload: building 2-layer pool (E16 H512 I256, 10 slots)")
+    layers = [to_gpu(small_layer(l, zipf=True)) for l in range(2)]
+    pool = OffloadedExperts(2, 16, 512, 256, 10, group_size=128, device="cuda")
+    for l, g in enumerate(layers):
+        pool.store_layer(l, g.experts)
+    torch.cuda.synchronize()
+    yield layers, pool
+    pool.close()
+
+
+def _slot_bytes_ok(pool: OffloadedExperts, layer: int, experts, blobs: torch.Tensor) -> None:
+    for e in set(int(v) for v in experts):
+        s = pool.cache.slot_of(layer, e)
+        assert s >= 0, f"expert {e} of layer {layer} not resident"
+        assert torch.equal(pool.device_pool[layer, s], blobs[e]), (layer, e, s)
+
+
+@pytest.mark.parametrize("path", ["decode", "gemv", "prefill"])
+def test_pooled_layer_matches_resident(pooled, path):
+    layers, pool = pooled
+    rng = np.random.default_rng(11)
+    for step, T in enumerate((1, 2, 1, 2, 2, 1)):
+        layer = step % 2
+        g = layers[layer]
+        _say(f"  pooled layer {layer} T={T} path={path}")
+        x = synth.make_tokens(T, 512, seed=100 + step).cuda()
+        ids, w, _, _ = ops.router_topk(x, g.router_w, 4, logit_bias=g.logit_bias)
+        # unrelated prefetches first, so demand has to evict and refetch
+        pool.prefetch(layer, rng.choice(16, size=3, replace=False).tolist())
+        pool.demand(layer, ids.cpu().reshape(-1).tolist())
+        got = ops.fused_experts(x, ids, w, pool.layer_experts(layer), path=path)
+        want = ops.fused_experts(x, ids, w, g.experts, path=path)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        _slot_bytes_ok(pool, layer, ids.cpu().reshape(-1).tolist(), pack_blobs(g.experts))
+
+
+def test_prefetch_then_demand_hits_and_bytes(pooled):
+    layers, pool = pooled
+    before = pool.stats()
+    issued = pool.prefetch(1, [13, 14, 15])
+    hits = pool.demand(1, [13, 14, 15])
+    torch.cuda.synchronize()
+    after = pool.stats()
+    assert hits == 3
+    assert after["prefetch_bytes"] - before["prefetch_bytes"] == issued * pool.blob
+    _slot_bytes_ok(pool, 1, [13, 14, 15], pack_blobs(layers[1].experts))
+
+
+def test_routed_layer_matches_oracle(pooled):
+    layers, pool = pooled
+    lay_cpu = small_layer(0, zipf=True)
+    x = synth.make_tokens(2, 512, seed=77)
+    out, ids_host = routed_layer(x.cuda(), layers[0].router_w, pool, 0, top_k=4,
+                                 logit_bias=layers[0].logit_bias)
+    torch.cuda.synchronize()
+    ref, r_ids, _, _ = moe_ref.moe_layer_ref(bf16_bits(x), bf16_bits(lay_cpu.router_w),
+                                             experts_to_np(lay_cpu.experts), top_k=4,
+                                             logit_bias=lay_cpu.logit_bias.numpy())
+    assert np.array_equal(ids_host.numpy(), r_ids)
+    assert moe_ref.rel_err(out.float().cpu().numpy(), ref) <= LAYER_RTOL
+
+
+@pytest.mark.parametrize("T,L,H,D,E,k", [(1, 3, 512, 256, 64, 16), (4, 2, 2048, 1024, 256, 16),
+                                          (3, 1, 256, 64, 40, 5)])
+def test_predictor_matches_oracle(T, L, H, D, E, k):
+    _say(f"predictor T={T} L={L} H={H} D={D} E={E} k={k}")
+    g = torch.Generator().manual_seed(T * 1000 + L)
+    h = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(L, D, H, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(L, E, D, generator=g) * 0.02).to(torch.bfloat16)
+    ids = ops.predictor_topk(h.cuda(), w1.cuda(), w2.cuda(), k).cpu().numpy()
+    r_ids, r_logits = moe_ref.predictor_ref(bf16_bits(h), bf16_bits(w1), bf16_bits(w2), k)
+    assert ids.shape == r_ids.shape
+    for l in range(L):
+        for t in range(T):
+            for j in range(k):
+                a, b = int(ids[l, t, j]), int(r_ids[l, t, j])
+                if a != b:
+                    la, lb = r_logits[l, t, a], r_logits[l, t, b]
+                    assert abs(la - lb) <= 1e-4 * max(abs(lb), 1e-3), (l, t, j, a, b, la, lb)
+
+
+def test_predictor_rejects_bad_shapes():
+    h = torch.zeros(1, 64, dtype=torch.bfloat16, device="cuda")
+    w1 = torch.zeros(2, 32, 64, dtype=torch.bfloat16, device="cuda")
+    w2 = torch.zeros(3, 16, 32, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.predictor_topk(h, w1, w2, 4)
