@@ -56,8 +56,26 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--offload-warmup", type=int, default=16)
     p.add_argument("--offload-slots", type=int, default=64, help="HBM slots per layer")
     p.add_argument("--prefetch-k", type=int, default=16, help="predicted experts prefetched per layer")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="first run a plain streaming kernel (fp32 negate) over this many MiB, three "
+                        "times: the known-size dispatch that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
     p.add_argument("--json-out", default=None, help="also write the full result JSON here")
     return p.parse_args()
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_decode_w1_bs64_hbm_traffic.md"
+
+
+def profiled_traffic(decode_path: str, batch: int) -> float | None:
+    """HBM bytes per W1 decode launch at batch 64 from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE scaled by a known-size streaming kernel); None when the run
+    measures another kernel or batch, or the summary is absent."""
+    if decode_path != "decode" or batch != 64 or not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def median_event_ms(fn, steps: int, stream) -> list[float]:
@@ -107,6 +125,17 @@ def main() -> int:
     torch.cuda.synchronize()
     resident = sum(ly.experts.nbytes_per_expert() * E for ly in layers)
     log(f"[bench] {L} layers resident: {resident / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration: 3 x negate of {args.copy_calibration_mib} MiB (reads and writes "
+            f"{n * 4} B each)")
+        del src, dst
 
     # ------------------------------------------------------------------ decode sweep
     graphs, decode = {}, {}
@@ -201,6 +230,7 @@ def main() -> int:
     w1_ms = statistics.median(median_event_ms(gw1.replay, args.steps, stream))
     w1_launch_us = w1_ms * 1e3 / L
     w1_bytes_per_launch = sum(r[3] for r in routed) * w1_per_expert / L
+    traffic = profiled_traffic(args.decode_path, Tr)
     roofline = {
         "bound": "hbm",
         "kernel": ("gemm_decode_kernel<W1>" if args.decode_path == "decode" else "gemv_decode_kernel<W1>")
@@ -208,7 +238,8 @@ def main() -> int:
         "achieved": w1_bytes_per_launch / (w1_launch_us * 1e-6) / 1e9,
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": TRAFFIC_PROFILE.name if traffic else None,
         "launch_us": w1_launch_us,
         "algorithmic_bytes_per_launch": w1_bytes_per_launch,
     }
