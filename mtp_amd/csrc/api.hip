@@ -159,6 +159,10 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
     MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
                                eids, ntpp, stream), "align");
   MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream), "w1");
+  if (path == MOE_PATH_DECODE && w2_token_sum_fits(ed, sd)) {
+    MOE_CHECK_HIP(launch_w2_token_sum(h, ed, sd, ids, w, out, stream), "w2 + sum");
+    return MOE_OK;
+  }
   MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
                 "w2");
   MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, out, stream), "moe_sum");
@@ -368,7 +372,7 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
                                      shared ? shared_gate_w : nullptr, logit_bias, logits, s),
                 "router logits");
   // decode-size batches: top-k and align in one block (no align launch)
-  const bool topk_aligned = path != MOE_PATH_PREFILL && T <= kTopkAlignMaxTokens && top_k <= 8;
+  const bool topk_aligned = path != MOE_PATH_PREFILL && topk_align_fits(T, top_k, shared ? 1 : 0);
   if (topk_aligned)
     MOE_CHECK_HIP(launch_topk_align(logits, T, E, top_k, shared ? 1 : 0, L.bm, L.cap, ids, w,
                                     at<int32_t>(workspace, L.sorted),

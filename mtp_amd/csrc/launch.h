@@ -20,9 +20,13 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
                                 hipStream_t stream);
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
                               int32_t* ids, float* weights, hipStream_t stream);
-// Top-k of every token and the align/sort in one 1024-thread block (T <= kTopkAlignMaxTokens,
-// top_k <= 8): the decode-size routing tail without a launch in between.
+// Top-k of every token (one wave each) and the align/sort of the at most 64 slots by one wave,
+// in one launch: the decode-size routing tail.
 constexpr int kTopkAlignMaxTokens = 8;
+inline bool topk_align_fits(int T, int top_k, int has_shared) {
+  return T >= 1 && T <= kTopkAlignMaxTokens && top_k <= 8 &&
+         T * top_k + (has_shared ? T : 0) <= 64;
+}
 hipError_t launch_topk_align(const float* logits, int T, int E, int top_k, int has_shared, int BM,
                              int cap, int32_t* ids, float* weights, int32_t* sorted, int32_t* eids,
                              int32_t* ntpp, hipStream_t stream);
@@ -51,6 +55,15 @@ hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const Slots
                             int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
 hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared, uint16_t* out,
                           hipStream_t stream);
+
+// W2 and the weighted sum in one kernel for one or two tokens (decode path): block = token x
+// column tile, one wave per slot of the token, out written directly (no ys, no sum kernel).
+constexpr int kTokenSumMaxTokens = 2;
+constexpr int kTokenSumMaxWaves = 9;  // top_k <= 8 plus the shared expert
+bool w2_token_sum_fits(const ExpertsDev& ed, const SlotsDev& sd);
+hipError_t launch_w2_token_sum(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                               const int32_t* ids, const float* topk_w, uint16_t* out,
+                               hipStream_t stream);
 
 // Prefill (bf16 MFMA) path.
 hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,

@@ -9,7 +9,7 @@
 //  * logits (any T; small tiles at decode for more waves in flight, 8 x 8 tiles at prefill for
 //    register reuse) - the tile shape never changes the per-(token, row) summation order;
 //  * top-k, one wave per token (any T);
-//  * top-k + align in one 1024-thread block for decode-size batches (T <= kTopkAlignMaxTokens):
+//  * top-k + align in one block for decode-size batches (at most 64 slots):
 //    the ids stay in LDS between the two steps, so no cross-block visibility is needed and the
 //    align launch disappears.
 #include "launch.h"
@@ -43,18 +43,18 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
              nullptr);
 }
 
-__global__ __launch_bounds__(1024) void topk_align_kernel(
+// One wave per token for the top-k, then wave 0 aligns the (at most 64) slots.
+__global__ __launch_bounds__(64 * kTopkAlignMaxTokens) void topk_align_kernel(
     const float* __restrict__ logits, int T, int E, int top_k, int has_shared, int BM, int cap,
     int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ sorted,
     int32_t* __restrict__ eids, int32_t* __restrict__ ntpp) {
-  __shared__ AlignSmem sm;
-  __shared__ int s_ids[kTopkAlignMaxTokens * 8];
+  __shared__ int s_ids[kAlignWaveMaxSlots];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int t = wave; t < T; t += 16)
-    topk_token(logits + (int64_t)t * (E + 1), E, top_k, has_shared, T, t, lane, ids, weights,
-               s_ids);
+  if (wave < T)
+    topk_token(logits + (int64_t)wave * (E + 1), E, top_k, has_shared, T, wave, lane, ids,
+               weights, s_ids);
   __syncthreads();
-  align_block(s_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, sm);
+  if (wave == 0) align_wave(s_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, lane);
 }
 
 template <int TT, int TE>
@@ -92,8 +92,8 @@ hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int 
 hipError_t launch_topk_align(const float* logits, int T, int E, int top_k, int has_shared, int BM,
                              int cap, int32_t* ids, float* weights, int32_t* sorted, int32_t* eids,
                              int32_t* ntpp, hipStream_t stream) {
-  if (T < 1 || T > kTopkAlignMaxTokens || top_k > 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(topk_align_kernel, dim3(1), dim3(1024), 0, stream, logits, T, E, top_k,
+  if (!topk_align_fits(T, top_k, has_shared)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(topk_align_kernel, dim3(1), dim3(64 * T), 0, stream, logits, T, E, top_k,
                      has_shared, BM, cap, ids, weights, sorted, eids, ntpp);
   return hipGetLastError();
 }

@@ -269,3 +269,49 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
     __builtin_amdgcn_wave_barrier();
   }
 }
+
+// Single-wave align for at most 64 slots (decode step sizes); same output as align_block.
+// Lane f holds slot f: the slots of one expert are found with a ballot match over the expert
+// id bits, the lowest lane of each group is its leader, and a group's offset is the sum of
+// the padded sizes of the groups with a smaller expert id (one pass over the leaders).
+constexpr int kAlignWaveMaxSlots = 64;
+
+MOE_DEV void align_wave(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
+                        int cap, int32_t* __restrict__ sorted, int32_t* __restrict__ eids,
+                        int32_t* __restrict__ ntpp, int lane) {
+  const int routed = T * top_k;
+  const int n_slots = routed + (has_shared ? T : 0);
+  const int e = (lane < n_slots) ? slot_expert(topk_ids, routed, E, lane) : -1;
+  const bool valid = e >= 0;
+  uint64_t peers = __ballot(valid);
+#pragma unroll
+  for (int bit = 0; bit < 10; ++bit) {
+    const bool b = valid && ((e >> bit) & 1);
+    const uint64_t bal = __ballot(b);
+    peers &= b ? bal : ~bal;
+  }
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int rank = __popcll(peers & lt_mask);
+  const int cnt = __popcll(peers);
+  const bool leader = valid && rank == 0;
+  const int padded = (cnt + BM - 1) / BM * BM;
+  uint64_t leaders = __ballot(leader);
+  int off = 0, total = 0;
+  while (leaders) {
+    const int j = __ffsll((long long)leaders) - 1;
+    leaders &= leaders - 1;
+    const int ej = __shfl(e, j, 64);
+    const int pj = __shfl(padded, j, 64);
+    total += pj;
+    if (valid && ej < e) off += pj;
+  }
+  const int limit = cap * BM;
+  if (valid && off + rank < limit) sorted[off + rank] = lane;
+  if (leader) {
+    for (int p = off + cnt; p < off + padded && p < limit; ++p) sorted[p] = n_slots;
+    for (int b = off / BM; b < (off + padded) / BM && b < cap; ++b) eids[b] = e;
+  }
+  for (int b = total / BM + lane; b < cap; b += 64) eids[b] = -1;
+  for (int p = total + lane; p < limit; p += 64) sorted[p] = n_slots;
+  if (lane == 0) *ntpp = total;
+}
