@@ -81,6 +81,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
 
   if (tid < BM) s_slot[tid] = sorted[b * BM + tid];
   __syncthreads();
+  // Valid rows come first in a block (an expert's slots, then its padding): the 16-row MFMA
+  // subtiles past them are all padding and are skipped (the tile is still dequantised once).
+  int nvalid = 0;
+#pragma unroll
+  for (int r = 0; r < BM; r += 16) nvalid += (unsigned)s_slot[r] < (unsigned)sd.num_slots ? 16 : 0;
+  const int mtiles = (nvalid - wm * 64 + 15) / 16;  // row subtiles of this wave with data
 
   // ---- A load mapping: 4 chunks of 16 B per thread; chunk = tid + 256 i -> row, k-chunk
   const uint16_t* a_row[4];
@@ -166,6 +172,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
       bf16x8_v af[4], bfr[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
+        if (mi >= mtiles) break;
         const int r = wm * 64 + mi * 16 + (lane & 15);
         af[mi] = *reinterpret_cast<const bf16x8_v*>(&lds_a[r * LDS_STRIDE + kofs]);
       }
@@ -179,10 +186,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
         bfr[ni] = *reinterpret_cast<const bf16x8_v*>(&lds_b[c * LDS_STRIDE + kofs]);
       }
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < 4; ++mi) {
+        if (mi >= mtiles) break;
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
+      }
     }
   }
 
