@@ -32,6 +32,141 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   logits_tile<TT, TE>(x, T, H, W, E, shared_w, bias, logits, t0, e0, lane);
 }
 
+// Prefill-size logits: one wave per 8 x 8 (token x router-row) tile, H a multiple of 512 (one
+// step = the 64 lanes' 16-byte chunks of every row). The summation order is the canonical one of
+// logits_tile: lane l owns chunks l, l + 64, ..., fma from +0.0f over chunks then elements. The
+// loads of step s + 1 are issued before the arithmetic of step s, and the kernel keeps at most
+// 256 VGPRs so two waves share each SIMD.
+//
+// The 64 per-lane partials are then combined by a transposed butterfly: at the step of lane
+// mask m every lane keeps the half of its values whose index bit matches its own lane bit and
+// adds the partner's (lane ^ m) copy of the same values. Every addition is the one the
+// butterfly v += shfl_xor(v, m) makes at that lane (the same two operands, and fp32 addition is
+// commutative), so the result is bit-identical, with 63 exchanges instead of 6 x 64. After the
+// last step lane l holds value l = (token i = l >> 3, row j = l & 7).
+constexpr int kRowsTileT = 8, kRowsTileE = 8;
+
+template <int N, int HALF>
+MOE_DEV void fold_swap32(float (&a)[N]) {
+#pragma unroll
+  for (int v = 0; v < HALF; ++v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[v]),
+                                                    __float_as_uint(a[v + HALF]), false, false);
+    a[v] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+template <int N, int HALF>
+MOE_DEV void fold_swap16(float (&a)[N]) {
+#pragma unroll
+  for (int v = 0; v < HALF; ++v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[v]),
+                                                    __float_as_uint(a[v + HALF]), false, false);
+    a[v] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// Lane mask M in {8, 4, 2, 1}: rows of 16 lanes, exchanged with DPP.
+template <int M, int N>
+MOE_DEV void fold_dpp(float (&a)[N], int lane) {
+  const bool up = (lane & M) != 0;
+#pragma unroll
+  for (int v = 0; v < M; ++v) {
+    const float keep = up ? a[v + M] : a[v];
+    const int send = __float_as_int(up ? a[v] : a[v + M]);
+    int recv;
+    if constexpr (M == 8) {
+      recv = __builtin_amdgcn_update_dpp(0, send, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (M == 4) {
+      recv = __shfl_xor(send, 4, 64);  // no single row DPP pattern pairs lane i with i ^ 4
+    } else if constexpr (M == 2) {
+      recv = __builtin_amdgcn_update_dpp(0, send, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else {
+      recv = __builtin_amdgcn_update_dpp(0, send, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    }
+    a[v] = keep + __int_as_float(recv);
+  }
+}
+
+MOE_DEV float bf16_elem(const u32x4& v, int el) {
+  return (el & 1) ? bf16hi_to_f32(v[el >> 1]) : bf16lo_to_f32(v[el >> 1]);
+}
+
+__global__ __launch_bounds__(256, 2) void router_logits_rows_kernel(
+    const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ W, int E,
+    const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
+    float* __restrict__ logits) {
+  constexpr int TT = kRowsTileT, TE = kRowsTileE;
+  const int rows = E + (shared_w ? 1 : 0);
+  const int lane = threadIdx.x & 63;
+  // wave index as a uniform (scalar) value: row pointers live in SGPRs, loads use saddr forms
+  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int tiles_e = (rows + TE - 1) / TE;
+  const int t0 = (wave / tiles_e) * TT;
+  const int e0 = (wave % tiles_e) * TE;
+  if (t0 >= T) return;
+  // Rows past the end are clamped to the last one (valid memory; their results are not stored).
+  const uint16_t* xr[TT];
+  const uint16_t* wr[TE];
+#pragma unroll
+  for (int i = 0; i < TT; ++i) xr[i] = x + (int64_t)min(t0 + i, T - 1) * H;
+#pragma unroll
+  for (int j = 0; j < TE; ++j) {
+    const int e = min(e0 + j, rows - 1);
+    wr[j] = e < E ? W + (int64_t)e * H : shared_w;
+  }
+  float acc[TT * TE];
+#pragma unroll
+  for (int v = 0; v < TT * TE; ++v) acc[v] = 0.0f;
+
+  u32x4 xa[TT], wa[TE], xb[TT], wb[TE];
+  auto load = [&](u32x4(&xv)[TT], u32x4(&wv)[TE], int step) {
+    const int off = step * 512 + lane * 8;
+#pragma unroll
+    for (int i = 0; i < TT; ++i) xv[i] = ld128(xr[i] + off);
+#pragma unroll
+    for (int j = 0; j < TE; ++j) wv[j] = ld128(wr[j] + off);
+  };
+  auto compute = [&](const u32x4(&xv)[TT], const u32x4(&wv)[TE]) {
+#pragma unroll
+    for (int el = 0; el < 8; ++el) {
+      float wf[TE];
+#pragma unroll
+      for (int j = 0; j < TE; ++j) wf[j] = bf16_elem(wv[j], el);
+#pragma unroll
+      for (int i = 0; i < TT; ++i) {
+        const float xf = bf16_elem(xv[i], el);
+#pragma unroll
+        for (int j = 0; j < TE; ++j) acc[i * TE + j] = __builtin_fmaf(xf, wf[j], acc[i * TE + j]);
+      }
+    }
+  };
+  const int nsteps = H / 512;
+  load(xa, wa, 0);
+  for (int s = 0; s < nsteps; s += 2) {
+    if (s + 1 < nsteps) load(xb, wb, s + 1);
+    compute(xa, wa);
+    if (s + 1 < nsteps) {
+      if (s + 2 < nsteps) load(xa, wa, s + 2);
+      compute(xb, wb);
+    }
+  }
+
+  fold_swap32<TT * TE, 32>(acc);
+  fold_swap16<TT * TE, 16>(acc);
+  fold_dpp<8>(acc, lane);
+  fold_dpp<4>(acc, lane);
+  fold_dpp<2>(acc, lane);
+  fold_dpp<1>(acc, lane);
+
+  const int t = t0 + (lane >> 3), e = e0 + (lane & 7);
+  if (t < T && e < rows) {
+    float v = acc[0];
+    if (bias && e < E) v = v + bias[e];
+    logits[(int64_t)t * (E + 1) + e] = v;
+  }
+}
+
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T,
                                                           int E, int top_k, int has_shared,
                                                           int32_t* __restrict__ ids,
@@ -77,6 +212,14 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
                                 hipStream_t stream) {
   if (T <= 4) return launch_logits_tiled<1, 2>(x, T, H, W, E, shared_w, bias, logits, stream);
   if (T <= 64) return launch_logits_tiled<2, 4>(x, T, H, W, E, shared_w, bias, logits, stream);
+  if (H % 512 == 0) {
+    const int rows = E + (shared_w ? 1 : 0);
+    const int tiles = ((T + kRowsTileT - 1) / kRowsTileT) * ((rows + kRowsTileE - 1) / kRowsTileE);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(router_logits_rows_kernel, dim3((tiles + 3) / 4), dim3(256), 0, stream, x,
+                       T, H, W, E, shared_w, bias, logits);
+    return hipGetLastError();
+  }
   return launch_logits_tiled<8, 8>(x, T, H, W, E, shared_w, bias, logits, stream);
 }
 

@@ -57,7 +57,9 @@ def test_dequant_reference_kat_and_g_idx():
                                                  (16, 256, 2048, 8, False, True),
                                                  (64, 256, 2048, 8, True, False),
                                                  (7, 16, 512, 4, False, True),
-                                                 (300, 256, 2048, 8, True, True)])
+                                                 (300, 256, 2048, 8, True, True),
+                                                 (129, 64, 1536, 8, False, True),
+                                                 (1024, 256, 2048, 8, True, False)])
 def test_router_bit_exact(T, E, H, k, zipf, shared):
     _say(f"router T={T} E={E} H={H} k={k} zipf={zipf} shared={shared}")
     x = synth.make_tokens(T, H, seed=7 + T)
