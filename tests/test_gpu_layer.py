@@ -58,6 +58,18 @@ def test_config1_full_shape(T, path):
     _check_layer(synth.make_layer(0), T, 8, path)
 
 
+@pytest.mark.parametrize("E,H,I,G,T,shared", [(32, 1024, 1024, 64, 200, True),
+                                               (16, 1536, 512, 256, 130, False),
+                                               (24, 512, 256, 128, 300, True)])
+def test_prefill_shapes_and_groups(E, H, I, G, T, shared):
+    """Prefill GEMMs over other hidden / intermediate sizes, group sizes 64 and 256, with and
+    without the shared expert (its block reads the shared projections)."""
+    _say(f"prefill shape E={E} H={H} I={I} G={G} T={T} shared={shared}")
+    layer = synth.make_layer(3, num_experts=E, hidden=H, intermediate=I, zipf=True, shared=shared,
+                             group=G)
+    _check_layer(layer, T, 4, "prefill")
+
+
 @pytest.mark.parametrize("T", [1, 32])
 def test_config4_shared_expert(T):
     """Config 4: routed top-8 plus a sigmoid-gated int4 shared expert."""
