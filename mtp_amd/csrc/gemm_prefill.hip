@@ -30,6 +30,11 @@ constexpr int LDS_STRIDE = BK + 8;  // bf16 per LDS row (16 B padding against ba
 constexpr int kMTiles = BM / 16;    // 8 row subtiles
 constexpr int kAChunks = BM * BK / 8 / 256;  // 16-byte A chunks per thread and step (8)
 
+// Buffer-resource word 3 for raw (unformatted, stride 0) buffers on gfx9; a byte offset at or
+// past num_records reads zeros without touching memory.
+constexpr int kBufferDword3 = 0x00020000;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
@@ -74,12 +79,21 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
     const uint16_t* __restrict__ A,  // W1: x [T, H]; W2: h [num_slots, I]
     ExpertsDev ed, SlotsDev sd, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ eids, const int32_t* __restrict__ ntpp,
-    const float* __restrict__ topk_w, uint16_t* __restrict__ h_out, float* __restrict__ ys) {
+    const float* __restrict__ topk_w, uint16_t* __restrict__ h_out, float* __restrict__ ys,
+    int a_bytes, int ncolblk) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * LDS_STRIDE];
   __shared__ int s_slot[BM];
 
-  const int b = blockIdx.y;
-  if (b * BM >= *ntpp) return;
+  // XCD-aware order: workgroup p runs on XCD p % 8, and XCD c takes the contiguous range
+  // [c S, c S + S) of the used (align block, column block) items, numbered expert-major, so the
+  // column blocks of one align block (same A rows) and the align blocks of one expert (same
+  // weights) run close together on one XCD and share its L2.
+  const int used = (*ntpp / BM) * ncolblk;
+  const int per_xcd = (used + 7) / 8;
+  const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= per_xcd || logical >= used) return;
+  const int b = logical / ncolblk;  // align block
+  const int cblk = logical % ncolblk;
   const int e = eids[b];
   if (!expert_ok(ed, e)) return;
 
@@ -105,10 +119,10 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   int col;  // first of the lane's 4 projection columns
   ProjDev p;
   if (MODE == MODE_W1) {
-    col = blockIdx.x * 128 + wave * 32 + 4 * (j & 7);
+    col = cblk * 128 + wave * 32 + 4 * (j & 7);
     p = (j < 8) ? (is_shared ? ed.sgate : ed.gate) : (is_shared ? ed.sup : ed.up);
   } else {
-    col = blockIdx.x * 256 + wave * 64 + 4 * j;
+    col = cblk * 256 + wave * 64 + 4 * j;
     p = is_shared ? ed.sdown : ed.down;
   }
   const ProjDev pr = proj_row(p, is_shared ? 0 : ed.row_stride, row, K8, NG, NOUT);
@@ -118,17 +132,18 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   const int zsh = 4 * (col & 7);
 
   // ---- A staging: chunk i of this thread = row (tid >> 4) + 16 i, 16-byte k-chunk tid & 15.
-  // Padding rows read the block's first row (always a slot) instead: every thread issues the
-  // same loads on every step, so the wait counts stay static, and the duplicates hit in L1.
-  // Their products land in rows that are never stored.
+  // Buffer loads: a padding row gets an out-of-range offset, which reads zeros without a memory
+  // access, while every thread still issues the same loads on every step (static wait counts).
   const int a_kc = tid & 15;
-  auto a_row_of = [&](int f) { return (MODE == MODE_W1) ? slot_token(sd, f) : f; };
-  const int a_first = a_row_of(s_slot[0]);
-  int a_off[kAChunks];  // element offset of the chunk's row in A
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, a_bytes, kBufferDword3);
+  uint32_t a_off[kAChunks];  // byte offset of the chunk in A
 #pragma unroll
   for (int i = 0; i < kAChunks; ++i) {
     const int f = s_slot[(tid >> 4) + 16 * i];
-    a_off[i] = (((unsigned)f < (unsigned)sd.num_slots) ? a_row_of(f) : a_first) * K + a_kc * 8;
+    const uint32_t ar = (MODE == MODE_W1) ? slot_token(sd, f) : f;
+    a_off[i] = ((unsigned)f < (unsigned)sd.num_slots) ? (ar * (uint32_t)K + a_kc * 8) * 2
+                                                       : kOutOfRange;
   }
 
   f32x4 acc[kMTiles][4];
@@ -144,7 +159,9 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   auto load_a = [&](int step, int half) {
 #pragma unroll
     for (int i = 0; i < kAChunks / 2; ++i)
-      ra[i] = ld128(A + a_off[half * (kAChunks / 2) + i] + step * BK);
+      ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            a_rsrc, a_off[half * (kAChunks / 2) + i] + step * BK * 2,
+                                            0, 0));
   };
   auto store_a = [&](uint16_t* la, int half) {
 #pragma unroll
@@ -159,7 +176,7 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
     gz[h].z = (uint32_t)bz[(int64_t)g * (NOUT / 8)];
   };
   auto load_bw = [&](int step, int kk) {
-    bw[kk] = ld128_nt(bq + (int64_t)(step * 16 + kk * 4) * NOUT);
+    bw[kk] = ld128(bq + (int64_t)(step * 16 + kk * 4) * NOUT);
   };
   load_gz(0, 0);
 #pragma unroll
@@ -254,6 +271,9 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   }
 }
 
+// Workgroups for up to `items` items, a multiple of 8 (each XCD gets the same number).
+int xcd_grid(int items) { return ((items + 7) / 8) * 8; }
+
 }  // namespace
 
 // Shapes (checked by the entry points): hidden % 512 == 0, intermediate in {256, 512, 1024},
@@ -261,11 +281,14 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
 hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int BMr, int cap, uint16_t* h, hipStream_t stream) {
-  if (BMr != BM || ed.hidden % BK != 0 || ed.inter % 128 != 0 || ed.group < 64)
+  const int64_t a_bytes = (int64_t)sd.T * ed.hidden * 2;  // x [T, H] bf16
+  if (BMr != BM || ed.hidden % BK != 0 || ed.inter % 128 != 0 || ed.group < 64 ||
+      a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
-  const dim3 grid(ed.inter / 128, cap);
-  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_W1>, grid, dim3(256), 0, stream, x, ed, sd, sorted,
-                     eids, ntpp, (const float*)nullptr, h, (float*)nullptr);
+  const int ncb = ed.inter / 128;
+  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_W1>, dim3(xcd_grid(cap * ncb)), dim3(256), 0, stream,
+                     x, ed, sd, sorted, eids, ntpp, (const float*)nullptr, h, (float*)nullptr,
+                     (int)a_bytes, ncb);
   return hipGetLastError();
 }
 
@@ -273,10 +296,13 @@ hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const Slot
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int BMr, int cap, const float* topk_w, float* ys,
                              hipStream_t stream) {
-  if (BMr != BM || ed.inter % BK != 0 || ed.hidden % 256 != 0 || ed.group < 64)
+  const int64_t a_bytes = (int64_t)sd.num_slots * ed.inter * 2;  // h [num_slots, I] bf16
+  if (BMr != BM || ed.inter % BK != 0 || ed.hidden % 256 != 0 || ed.group < 64 ||
+      a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
-  const dim3 grid(ed.hidden / 256, cap);
-  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_W2>, grid, dim3(256), 0, stream, h, ed, sd, sorted,
-                     eids, ntpp, topk_w, (uint16_t*)nullptr, ys);
+  const int ncb = ed.hidden / 256;
+  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_W2>, dim3(xcd_grid(cap * ncb)), dim3(256), 0, stream,
+                     h, ed, sd, sorted, eids, ntpp, topk_w, (uint16_t*)nullptr, ys, (int)a_bytes,
+                     ncb);
   return hipGetLastError();
 }
