@@ -139,7 +139,9 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
                    float* ys, int32_t path, void* stream);
 
 /* out[t, :] = bf16(sum_{i<top_k} ys[t*top_k + i, :] (+ ys[T*top_k + t, :])), fixed order.
- * Replaces ops.moe_sum (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19801-19804). */
+ * Replaces ops.moe_sum (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19801-19804).
+ * Sums every slot: moe_w2_down_v1 leaves the ys rows of dropped slots (see
+ * moe_fused_experts_v1) unwritten, so a caller that may drop slots zeroes ys first. */
 int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
                uint16_t* out, void* stream);
 
@@ -161,7 +163,10 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
 
 /* Experts with caller-given routing: topk_ids int32 [T, top_k], topk_weights fp32 [T, top_k].
  * Replaces TopKExpertMlp.forward (src/mtp_expert_prefetch/repack/gptq_unpack.py:293-327)
- * and moe_tokens with given ids (src/mtp_expert_prefetch/mtp/extra_tensors.py:544-598). */
+ * and moe_tokens with given ids (src/mtp_expert_prefetch/mtp/extra_tensors.py:544-598).
+ * A slot is dropped (contributes zero) when its id is outside [0, num_experts) or, with an
+ * expert_row map, names an expert whose row is negative (not resident), as the reference drops
+ * ids outside [0, E) and unmapped experts (vllm_router_trace.py:14138-14153). */
 int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
                          const float* topk_weights, int32_t top_k,
                          const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
@@ -201,7 +206,8 @@ typedef struct moe_slot_cache_desc_v1 {
   int64_t expert_bytes;
   const void* host_pool;      /* pinned host [num_layers][num_experts][expert_bytes] */
   void* device_pool;          /* device [num_layers][slots_per_layer][expert_bytes] */
-  int32_t* device_expert_row; /* device [num_layers][num_experts]: expert -> slot */
+  int32_t* device_expert_row; /* device [num_layers][num_experts]: expert -> slot, -1 when not
+                               resident (its slots are dropped); the caller initialises it */
   int32_t dry_run;
   int32_t reserved;
 } moe_slot_cache_desc_v1;

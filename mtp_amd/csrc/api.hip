@@ -165,7 +165,9 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   }
   MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
                 "w2");
-  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, out, stream), "moe_sum");
+  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, ids, ex->num_experts,
+                               ex->expert_row, out, stream),
+                "moe_sum");
   return MOE_OK;
 }
 
@@ -333,7 +335,8 @@ int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_
     return fail(MOE_ERR_SHAPE, "moe_sum: T=%d top_k=%d hidden=%d", T, top_k, hidden);
   if (T == 0) return MOE_OK;
   if (!ys || !out) return fail(MOE_ERR_NULL, "moe_sum: NULL pointer");
-  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, hidden, has_shared ? 1 : 0, out, (hipStream_t)stream),
+  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, hidden, has_shared ? 1 : 0, nullptr, 0, nullptr, out,
+                               (hipStream_t)stream),
                 "moe_sum");
   return MOE_OK;
 }

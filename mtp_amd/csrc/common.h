@@ -96,9 +96,19 @@ MOE_DEV ProjDev proj_row(const ProjDev& p, int64_t stride_bytes, int64_t row, in
                  p.scales + row * NG * NOUT};
 }
 
-// A block's expert id is usable: a routed expert, or the shared expert when one is present.
+// A routed slot's expert contributes: its id is in [0, num_experts) and, with an expert_row map
+// (a slot pool), it is resident (row >= 0). Other slots are dropped and contribute zero, as the
+// reference drops ids outside [0, E) and unmapped experts
+// (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:14138-14153).
+MOE_DEV bool routed_ok(const int32_t* expert_row, int num_experts, int e) {
+  return e >= 0 && e < num_experts && (expert_row == nullptr || expert_row[e] >= 0);
+}
+
+// A block's expert id is usable: a contributing routed expert, or the shared expert when one is
+// present.
 MOE_DEV bool expert_ok(const ExpertsDev& ed, int e) {
-  return (e >= 0 && e < ed.num_experts) || (e == ed.num_experts && ed.sgate.qweight != nullptr);
+  return routed_ok(ed.expert_row, ed.num_experts, e) ||
+         (e == ed.num_experts && ed.sgate.qweight != nullptr);
 }
 
 MOE_DEV int64_t expert_row(const ExpertsDev& ed, int e) {

@@ -367,7 +367,7 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
   const bool is_shared = i >= sd.top_k;
   const int f = is_shared ? sd.T * sd.top_k + t : t * sd.top_k + i;
   const int e = is_shared ? ed.num_experts : ids[f];
-  const bool ok = is_shared || (e >= 0 && e < ed.num_experts);
+  const bool ok = is_shared || routed_ok(ed.expert_row, ed.num_experts, e);
   const int G = ed.group, K = ed.inter, NOUT = ed.hidden;
   const int m = lane & 15, kq = lane >> 4;
   const int cl = blockIdx.x * TW + CT * m;
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
   f32x4 acc[CT];
 #pragma unroll
   for (int j = 0; j < CT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (ok) {  // wave-uniform: an id outside [0, num_experts) contributes nothing
+  if (ok) {  // wave-uniform: a dropped slot contributes nothing
     const int64_t row = is_shared ? 0 : expert_row(ed, e);
     ProjDev pj[1];
     projections(ed, DEC_W2, is_shared, pj);

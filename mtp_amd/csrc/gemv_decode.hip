@@ -223,16 +223,25 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(const uint16_t* __rest
 }
 
 // ------------------------------------------------------------------------------- moe_sum
+// out[t] = bf16(sum over the token's slots in order of ys[slot]). With `ids`, routed slots whose
+// expert is dropped (routed_ok false: their ys rows were never written) are skipped.
 __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ ys, int T,
                                                       int top_k, int H, int has_shared,
+                                                      const int32_t* __restrict__ ids,
+                                                      int num_experts,
+                                                      const int32_t* __restrict__ expert_row,
                                                       uint16_t* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int per_row = H / 4;
   const int64_t t = idx / per_row;
   if (t >= T) return;
   const int c = (int)(idx % per_row) * 4;
-  f32x4 s = *reinterpret_cast<const f32x4*>(ys + (t * top_k) * H + c);
-  for (int i = 1; i < top_k; ++i) s += *reinterpret_cast<const f32x4*>(ys + (t * top_k + i) * H + c);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < top_k; ++i) {
+    const int64_t f = t * top_k + i;
+    if (ids && !routed_ok(expert_row, num_experts, ids[f])) continue;
+    s += *reinterpret_cast<const f32x4*>(ys + f * H + c);
+  }
   if (has_shared) s += *reinterpret_cast<const f32x4*>(ys + ((int64_t)T * top_k + t) * H + c);
   u32x2 o;
   o[0] = pack_bf16x2(s[0], s[1]);
@@ -263,11 +272,12 @@ hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const Slots
   return hipGetLastError();
 }
 
-hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared, uint16_t* out,
-                          hipStream_t stream) {
+hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared,
+                          const int32_t* ids, int num_experts, const int32_t* expert_row,
+                          uint16_t* out, hipStream_t stream) {
   const int64_t n = (int64_t)T * (H / 4);
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(moe_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ys,
-                     T, top_k, H, has_shared, out);
+                     T, top_k, H, has_shared, ids, num_experts, expert_row, out);
   return hipGetLastError();
 }

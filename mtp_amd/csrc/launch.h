@@ -53,8 +53,10 @@ hipError_t launch_w1_decode(const uint16_t* x, const ExpertsDev& ed, const Slots
 hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                             const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                             int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
-hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared, uint16_t* out,
-                          hipStream_t stream);
+// ids == nullptr: every slot is summed; otherwise routed slots with a dropped expert are skipped.
+hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared,
+                          const int32_t* ids, int num_experts, const int32_t* expert_row,
+                          uint16_t* out, hipStream_t stream);
 
 // W2 and the weighted sum in one kernel for one or two tokens (decode path): block = token x
 // column tile, one wave per slot of the token, out written directly (no ys, no sum kernel).

@@ -273,7 +273,8 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
     c->staging_next = (r + 1) % kStagingRing;
     SC_HIP(hipEventSynchronize(c->staging_done[r]), "staging reuse");
     int32_t* stage = c->staging + (size_t)r * c->d.num_experts;
-    for (int e = 0; e < c->d.num_experts; ++e) stage[e] = L.slot_of[e] >= 0 ? L.slot_of[e] : 0;
+    // -1 for experts that are not resident: the kernels drop their slots (never read row -1)
+    for (int e = 0; e < c->d.num_experts; ++e) stage[e] = L.slot_of[e];
     SC_HIP(hipMemcpyAsync(c->d.device_expert_row + (size_t)layer * c->d.num_experts, stage,
                           (size_t)c->d.num_experts * 4, hipMemcpyHostToDevice, cs), "table upload");
     SC_HIP(hipEventRecord(c->staging_done[r], cs), "record staging");

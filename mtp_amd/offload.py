@@ -206,8 +206,9 @@ class OffloadedExperts:
         self.host = PinnedHostBuffer(num_layers * num_experts * self.blob)
         self.device_pool = torch.empty(num_layers, max(slots_per_layer, 1), self.blob,
                                        dtype=torch.uint8, device=self.device)
-        self.expert_row = torch.zeros(num_layers, num_experts, dtype=torch.int32,
-                                      device=self.device)
+        # expert -> slot table; -1 = not resident (kernels drop such slots)
+        self.expert_row = torch.full((num_layers, num_experts), -1, dtype=torch.int32,
+                                     device=self.device)
         self.cache = SlotCache(num_layers, num_experts, slots_per_layer, self.blob,
                                host_pool=self.host.ptr, device_pool=self.device_pool.data_ptr(),
                                expert_row=self.expert_row.data_ptr(),
@@ -235,6 +236,7 @@ class OffloadedExperts:
         """Forget every resident slot and counter (pools are kept; the next demands refetch)."""
         torch.cuda.synchronize(self.device)
         self.cache.close()
+        self.expert_row.fill_(-1)
         self.cache = SlotCache(self.num_layers, self.num_experts, self.slots, self.blob,
                                host_pool=self.host.ptr, device_pool=self.device_pool.data_ptr(),
                                expert_row=self.expert_row.data_ptr(),
@@ -269,6 +271,7 @@ class OffloadedExperts:
     def close(self) -> None:
         torch.cuda.synchronize(self.device)
         self.cache.close()
+        self.expert_row.fill_(-1)
         self.host.close()
 
 

@@ -180,19 +180,24 @@ def expert_mlp_f32(x: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torc
 
 
 def moe_layer_f32(x_bits: np.ndarray, ids: np.ndarray, weights: np.ndarray, layer: dict,
-                  *, shared: dict | None = None, shared_gate_values: np.ndarray | None = None) -> np.ndarray:
+                  *, shared: dict | None = None, shared_gate_values: np.ndarray | None = None,
+                  dropped: frozenset[int] = frozenset()) -> np.ndarray:
     """fp32-accumulated top-k expert sum (+ gated shared expert), slot order i = 0..k-1.
 
-    layer holds numpy arrays keyed '{proj}.{kind}' stacked over experts [E, ...].
+    layer holds numpy arrays keyed '{proj}.{kind}' stacked over experts [E, ...]. A slot whose
+    id is outside [0, E), or names an expert in `dropped`, contributes nothing (the reference
+    drops ids outside [0, E) and unmapped experts, vllm_router_trace.py:14138-14153).
     """
     x = torch.from_numpy(gptq_ref.bf16_bits_to_f32(x_bits))
     T, H = x.shape
+    E = layer["gate_proj.qweight"].shape[0]
     out = torch.zeros(T, H, dtype=torch.float32)
-    cache: dict[int, tuple] = {}
-    for e in np.unique(ids):
-        cache[int(e)] = dequant_expert(layer, int(e))
+    keep = [int(e) for e in np.unique(ids) if 0 <= int(e) < E and int(e) not in dropped]
+    cache: dict[int, tuple] = {e: dequant_expert(layer, e) for e in keep}
     for i in range(ids.shape[1]):
         for e in np.unique(ids[:, i]):
+            if int(e) not in cache:
+                continue
             rows = np.nonzero(ids[:, i] == e)[0]
             y = expert_mlp_f32(x[rows], *cache[int(e)])
             out[rows] += torch.from_numpy(weights[rows, i]).float()[:, None] * y

@@ -160,3 +160,26 @@ def test_layer_is_deterministic():
     x = synth.make_tokens(32, seed=5).cuda()
     outs = [ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias) for _ in range(3)]
     assert all(torch.equal(outs[0], o) for o in outs[1:])
+
+
+@pytest.mark.parametrize("path,T", [("decode", 1), ("decode", 2), ("decode", 5), ("gemv", 5),
+                                    ("prefill", 64), ("decode", 64)])
+def test_dropped_slots_contribute_zero(path, T):
+    """Ids outside [0, E) are dropped (reference: vllm_router_trace.py:14138-14153); the other
+    slots of the token still count, on every path including the fused W2 + sum."""
+    _say(f"dropped slots path={path} T={T}")
+    lay = small_layer(4)
+    g = to_gpu(lay)
+    rng = np.random.default_rng(40 + T)
+    ids = np.stack([rng.choice(16, size=4, replace=False) for _ in range(T)]).astype(np.int32)
+    drop = rng.random(ids.shape) < 0.3
+    ids[drop] = rng.choice([-1, 16, 40], size=int(drop.sum()))
+    w = rng.uniform(0.1, 1.0, size=ids.shape).astype(np.float32)
+    x = synth.make_tokens(T, 512, seed=41 + T)
+    got = ops.fused_experts(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
+                            g.experts, path=path)
+    torch.cuda.synchronize()
+    ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(lay.experts))
+    err = moe_ref.rel_err(got.float().cpu().numpy(), ref)
+    _say(f"  rel_err={err:.3e}")
+    assert np.isfinite(err) and err <= LAYER_RTOL

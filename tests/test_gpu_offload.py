@@ -118,3 +118,30 @@ def test_predictor_rejects_bad_shapes():
     w2 = torch.zeros(3, 16, 32, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError):
         ops.predictor_topk(h, w1, w2, 4)
+
+
+@pytest.mark.parametrize("path", ["decode", "gemv", "prefill"])
+def test_nonresident_expert_is_dropped(pooled, path):
+    """A pool view maps experts that are not resident to row -1: their slots contribute zero
+    (never a read through a negative row)."""
+    layers, pool = pooled
+    layer = 1
+    g = layers[layer]
+    pool.demand(layer, [0, 1, 2, 3, 4, 5])
+    absent = [e for e in range(16) if pool.cache.slot_of(layer, e) < 0]
+    assert absent, "the 10-slot pool cannot hold all 16 experts"
+    e_nr = absent[0]
+    _say(f"  non-resident expert {e_nr} path={path}")
+    T = 3
+    ids = np.array([[0, 1, e_nr, 2], [e_nr, 3, 4, 5], [5, 4, 3, e_nr]], dtype=np.int32)
+    w = np.full(ids.shape, 0.25, dtype=np.float32)
+    x = synth.make_tokens(T, 512, seed=77)
+    got = ops.fused_experts(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
+                            pool.layer_experts(layer), path=path)
+    torch.cuda.synchronize()
+    lay_cpu = small_layer(layer, zipf=True)
+    ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(lay_cpu.experts),
+                                dropped=frozenset({e_nr}))
+    err = moe_ref.rel_err(got.float().cpu().numpy(), ref)
+    _say(f"  rel_err={err:.3e}")
+    assert np.isfinite(err) and err <= LAYER_RTOL
