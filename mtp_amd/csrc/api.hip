@@ -140,11 +140,18 @@ Workspace layout(int T, int top_k, const moe_expert_set_v1* ex, int has_shared, 
 template <typename T>
 T* at(void* base, size_t off) { return reinterpret_cast<T*>(static_cast<char*>(base) + off); }
 
-// [align ->] W1 -> W2 -> top-k sum over a routed workspace (ids and weights in place; when
-// `aligned` the sorted slot layout is in place too).
+// How run_experts finds each slot's expert.
+enum Routing {
+  ROUTE_ALIGN,          // ids/weights in place: align, then the blocked kernels
+  ROUTE_ALIGNED,        // the sorted slot layout is in place too
+  ROUTE_GRID_LOGITS,    // slot grid: W1 computes the top-k from the logits and publishes it
+  ROUTE_GRID_IDS        // slot grid over the ids/weights in place
+};
+
+// [align ->] W1 -> W2 -> top-k sum over a routed workspace.
 int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex,
                 const moe_expert_set_v1* sh, const Workspace& L, void* ws, uint16_t* out,
-                int path, bool aligned, hipStream_t stream) {
+                int path, Routing routing, hipStream_t stream) {
   const int has_shared = sh ? 1 : 0;
   const ExpertsDev ed = make_experts_dev(ex, sh);
   SlotsDev sd{T, top_k, T * top_k + (has_shared ? T : 0)};
@@ -155,16 +162,26 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   int32_t* ntpp = at<int32_t>(ws, L.ntpp);
   uint16_t* h = at<uint16_t>(ws, L.h);
   float* ys = at<float>(ws, L.ys);
-  if (!aligned)
-    MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
-                               eids, ntpp, stream), "align");
-  MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream), "w1");
+  const bool grid = routing == ROUTE_GRID_LOGITS || routing == ROUTE_GRID_IDS;
+  if (grid) {
+    const SlotGrid sg{1, routing == ROUTE_GRID_LOGITS ? at<float>(ws, L.logits) : nullptr, ids, w};
+    MOE_CHECK_HIP(launch_w1_decode_slotgrid(x, ed, sd, sg, h, stream), "w1 (slot grid)");
+  } else {
+    if (routing == ROUTE_ALIGN)
+      MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
+                                 eids, ntpp, stream), "align");
+    MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream), "w1");
+  }
   if (path == MOE_PATH_DECODE && w2_token_sum_fits(ed, sd)) {
     MOE_CHECK_HIP(launch_w2_token_sum(h, ed, sd, ids, w, out, stream), "w2 + sum");
     return MOE_OK;
   }
-  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
-                "w2");
+  if (grid)
+    MOE_CHECK_HIP(launch_w2_decode_slotgrid(h, ed, sd, SlotGrid{1, nullptr, ids, w}, ys, stream),
+                  "w2 (slot grid)");
+  else
+    MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
+                  "w2");
   MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, ids, ex->num_experts,
                                ex->expert_row, out, stream),
                 "moe_sum");
@@ -374,17 +391,24 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E,
                                      shared ? shared_gate_w : nullptr, logit_bias, logits, s),
                 "router logits");
-  // decode-size batches: top-k and align in one block (no align launch)
-  const bool topk_aligned = path != MOE_PATH_PREFILL && topk_align_fits(T, top_k, shared ? 1 : 0);
-  if (topk_aligned)
+  // decode-size batches: with one or two tokens the MFMA decode kernels compute the top-k
+  // themselves (slot grid; every W1 workgroup repeats it, which costs more than the launch it
+  // saves beyond two tokens); otherwise top-k and align come from one block (no align launch)
+  const bool small = topk_align_fits(T, top_k, shared ? 1 : 0);
+  Routing routing = ROUTE_ALIGN;
+  if (path == MOE_PATH_DECODE && small && T <= kTokenSumMaxTokens) {
+    routing = ROUTE_GRID_LOGITS;
+  } else if (path != MOE_PATH_PREFILL && small) {
     MOE_CHECK_HIP(launch_topk_align(logits, T, E, top_k, shared ? 1 : 0, L.bm, L.cap, ids, w,
                                     at<int32_t>(workspace, L.sorted),
                                     at<int32_t>(workspace, L.eids),
                                     at<int32_t>(workspace, L.ntpp), s), "router topk+align");
-  else
+    routing = ROUTE_ALIGNED;
+  } else {
     MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, shared ? 1 : 0, ids, w, s),
                   "router topk");
-  rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, topk_aligned, s);
+  }
+  rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, routing, s);
   if (rc) return rc;
   if (topk_ids_out)
     MOE_CHECK_HIP(hipMemcpyAsync(topk_ids_out, ids, (size_t)T * top_k * 4,
@@ -422,7 +446,10 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
   if (shared)
     MOE_CHECK_HIP(launch_shared_gate(x, T, experts->hidden, shared_gate_w, top_k,
                                      at<float>(workspace, L.logits), w, s), "shared gate");
-  return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, false, s);
+  const Routing routing = (path == MOE_PATH_DECODE && slot_grid_fits(T, top_k, shared ? 1 : 0))
+                              ? ROUTE_GRID_IDS
+                              : ROUTE_ALIGN;
+  return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, routing, s);
 }
 
 }  // extern "C"

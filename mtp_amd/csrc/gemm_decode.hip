@@ -34,6 +34,7 @@
 
 #include "common.h"
 #include "launch.h"
+#include "routing.h"
 
 namespace {
 
@@ -258,23 +259,62 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
     const uint16_t* __restrict__ act, ExpertsDev ed, SlotsDev sd,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ eids,
     const int32_t* __restrict__ ntpp, const float* __restrict__ topk_w,
-    uint16_t* __restrict__ h_out, float* __restrict__ ys) {
+    uint16_t* __restrict__ h_out, float* __restrict__ ys, SlotGrid sg) {
   constexpr int NP = (MODE == DEC_W1) ? 2 : 1;  // projections (gate, up) or (down)
   constexpr int NT = NP * CT;                    // MFMA N-subtiles per lane
   constexpr int TW = 16 * CT;                    // columns per block
   __shared__ float red[(KS > 1 ? KS - 1 : 1) * NT * 4 * 64];
 
-  // Block metadata: every load below is in bounds for any b < gridDim.y, so all of them are
-  // issued together (one memory latency before the first weight load, not a chain).
-  const int b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n_padded = *ntpp;
-  const int e = eids[b];
-  const int f_m = sorted[b * kBM + (lane & 15)];        // A row of this lane
-  int f_out[4];                                         // D rows of this lane
+  int e, f_m, f_out[4];  // expert; A row of this lane; D rows of this lane
+  if (sg.active) {
+    // Slot grid (SlotGrid in launch.h): slots from the routed ids, no align pass.
+    __shared__ int s_ids[kSlotGridMaxSlots];
+    __shared__ float s_w[kSlotGridMaxSlots + kTopkAlignMaxTokens];
+    __shared__ int s_rows[kBM];
+    const int E = ed.num_experts, routed = sd.T * sd.top_k, n_slots = sd.num_slots;
+    if (sg.logits) {  // every workgroup computes the same top-k of the (at most 8) tokens
+      for (int t = wave; t < sd.T; t += KS) {
+        const float* row = sg.logits + (int64_t)t * (E + 1);
+        topk_token_lds(row, E, sd.top_k, lane, s_ids + t * sd.top_k, s_w + t * sd.top_k);
+        if (n_slots > routed && lane == 0) s_w[routed + t] = 1.0f / (1.0f + expf(-row[E]));
+      }
+    } else if (tid < routed) {
+      s_ids[tid] = sg.ids[tid];
+    }
+    __syncthreads();
+    if (sg.logits && blockIdx.x == 0 && blockIdx.y == 0) {  // publish for W2 and the caller
+      if (tid < routed) sg.ids[tid] = s_ids[tid];
+      if (tid < n_slots) sg.weights[tid] = s_w[tid];
+    }
+    const int b = blockIdx.y;  // slot index
+    auto expert_of = [&](int f) { return f < routed ? s_ids[f] : E; };
+    e = expert_of(b);
+    const uint64_t mask = __ballot(lane < n_slots && expert_of(lane) == e);
+    const int rank_b = __popcll(mask & ((1ull << b) - 1));  // occurrences of e before slot b
+    if (rank_b % kBM != 0 || !expert_ok(ed, e)) return;   // uniform over the workgroup
+    const int rank = __popcll(mask & ((1ull << lane) - 1));
+    if (wave == 0 && ((mask >> lane) & 1) && rank >= rank_b && rank < rank_b + kBM)
+      s_rows[rank - rank_b] = lane;
+    const int cnt = min(__popcll(mask) - rank_b, kBM);
+    __syncthreads();
+    f_m = (lane & 15) < cnt ? s_rows[lane & 15] : n_slots;
 #pragma unroll
-  for (int el = 0; el < 4; ++el) f_out[el] = sorted[b * kBM + 4 * (lane >> 4) + el];
-  if (b * kBM >= n_padded || !expert_ok(ed, e)) return;
+    for (int el = 0; el < 4; ++el) {
+      const int r = 4 * (lane >> 4) + el;
+      f_out[el] = r < cnt ? s_rows[r] : n_slots;
+    }
+  } else {
+    // Block metadata: every load below is in bounds for any b < gridDim.y, so all of them are
+    // issued together (one memory latency before the first weight load, not a chain).
+    const int b = blockIdx.y;
+    const int n_padded = *ntpp;
+    e = eids[b];
+    f_m = sorted[b * kBM + (lane & 15)];
+#pragma unroll
+    for (int el = 0; el < 4; ++el) f_out[el] = sorted[b * kBM + 4 * (lane >> 4) + el];
+    if (b * kBM >= n_padded || !expert_ok(ed, e)) return;
+  }
 
   const int G = ed.group;
   const int K = (MODE == DEC_W1) ? ed.hidden : ed.inter;
@@ -400,22 +440,24 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
 template <int MODE, int SPG, int KS, int CT, int NB>
 hipError_t launch_cfg(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int cap,
-                      const float* topk_w, uint16_t* h, float* ys, hipStream_t stream) {
+                      const float* topk_w, uint16_t* h, float* ys, const SlotGrid& sg,
+                      hipStream_t stream) {
   const int NOUT = (MODE == DEC_W1) ? ed.inter : ed.hidden;
-  const dim3 grid(NOUT / (16 * CT), cap);
+  const dim3 grid(NOUT / (16 * CT), sg.active ? sd.num_slots : cap);
   hipLaunchKernelGGL((gemm_decode_kernel<MODE, SPG, KS, CT, NB>), grid, dim3(64 * KS), 0, stream,
-                     act, ed, sd, sorted, eids, ntpp, topk_w, h, ys);
+                     act, ed, sd, sorted, eids, ntpp, topk_w, h, ys, sg);
   return hipGetLastError();
 }
 
 template <int MODE, int KS, int CT, int NB>
 hipError_t launch_group(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
                         const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int cap,
-                        const float* topk_w, uint16_t* h, float* ys, hipStream_t stream) {
+                        const float* topk_w, uint16_t* h, float* ys, const SlotGrid& sg,
+                        hipStream_t stream) {
   switch (ed.group) {
-    case 64: return launch_cfg<MODE, 2, KS, CT, NB>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, stream);
-    case 128: return launch_cfg<MODE, 4, KS, CT, NB>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, stream);
-    case 256: return launch_cfg<MODE, 8, KS, CT, NB>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, stream);
+    case 64: return launch_cfg<MODE, 2, KS, CT, NB>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, sg, stream);
+    case 128: return launch_cfg<MODE, 4, KS, CT, NB>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, sg, stream);
+    case 256: return launch_cfg<MODE, 8, KS, CT, NB>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, sg, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -425,7 +467,7 @@ template <int MODE>
 hipError_t launch_decode_cfg(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int cap, const float* topk_w, uint16_t* h, float* ys, int ks, int ct,
-                             int nb, hipStream_t stream) {
+                             int nb, const SlotGrid& sg, hipStream_t stream) {
   const int K = (MODE == DEC_W1) ? ed.hidden : ed.inter;
   const int NOUT = (MODE == DEC_W1) ? ed.inter : ed.hidden;
   if ((ct != 2 && ct != 4) || NOUT % (16 * ct) != 0 || K % (ks * ed.group) != 0)
@@ -434,7 +476,7 @@ hipError_t launch_decode_cfg(const uint16_t* act, const ExpertsDev& ed, const Sl
 #define MOE_DEC_CASE(KSV, CTV, NBV)                                                             \
   if (ks == KSV && ct == CTV && nb == NBV)                                                      \
     return launch_group<MODE, KSV, CTV, NBV>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h,  \
-                                             ys, stream);
+                                             ys, sg, stream);
   MOE_DEC_CASE(1, 2, 2) MOE_DEC_CASE(2, 2, 2) MOE_DEC_CASE(4, 2, 2) MOE_DEC_CASE(8, 2, 2)
   MOE_DEC_CASE(1, 4, 2) MOE_DEC_CASE(2, 4, 2) MOE_DEC_CASE(4, 4, 2)
   MOE_DEC_CASE(1, 2, 3) MOE_DEC_CASE(2, 2, 3) MOE_DEC_CASE(4, 2, 3)
@@ -492,30 +534,52 @@ hipError_t launch_token_sum(const uint16_t* h, const ExpertsDev& ed, const Slots
 
 }  // namespace
 
+namespace {
+template <int MODE>
+hipError_t launch_decode_picked(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
+                                const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                                int cap, const float* topk_w, uint16_t* h, float* ys,
+                                const SlotGrid& sg, hipStream_t stream) {
+  int ks, ct, nb;
+  pick_decode_cfg<MODE>(ed, sd, &ks, &ct, &nb);
+  hipError_t e = launch_decode_cfg<MODE>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, ks,
+                                         ct, nb, sg, stream);
+  if (e == hipErrorInvalidValue)  // shape outside the tuned set: one wave, double-buffered
+    e = launch_decode_cfg<MODE>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, 1, 2, 2, sg,
+                                stream);
+  return e;
+}
+}  // namespace
+
 hipError_t launch_w1_decode_mfma(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                                  const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                                  int cap, uint16_t* h, hipStream_t stream) {
-  int ks, ct, nb;
-  pick_decode_cfg<DEC_W1>(ed, sd, &ks, &ct, &nb);
-  hipError_t e = launch_decode_cfg<DEC_W1>(x, ed, sd, sorted, eids, ntpp, cap, nullptr, h, nullptr,
-                                           ks, ct, nb, stream);
-  if (e == hipErrorInvalidValue)  // shape outside the tuned set: one wave, double-buffered
-    e = launch_decode_cfg<DEC_W1>(x, ed, sd, sorted, eids, ntpp, cap, nullptr, h, nullptr, 1, 2,
-                                  2, stream);
-  return e;
+  return launch_decode_picked<DEC_W1>(x, ed, sd, sorted, eids, ntpp, cap, nullptr, h, nullptr,
+                                      SlotGrid{0, nullptr, nullptr, nullptr}, stream);
 }
 
 hipError_t launch_w2_decode_mfma(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                  const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                                  int cap, const float* topk_w, float* ys, hipStream_t stream) {
-  int ks, ct, nb;
-  pick_decode_cfg<DEC_W2>(ed, sd, &ks, &ct, &nb);
-  hipError_t e = launch_decode_cfg<DEC_W2>(h, ed, sd, sorted, eids, ntpp, cap, topk_w, nullptr, ys,
-                                           ks, ct, nb, stream);
-  if (e == hipErrorInvalidValue)
-    e = launch_decode_cfg<DEC_W2>(h, ed, sd, sorted, eids, ntpp, cap, topk_w, nullptr, ys, 1, 2, 2,
-                                  stream);
-  return e;
+  return launch_decode_picked<DEC_W2>(h, ed, sd, sorted, eids, ntpp, cap, topk_w, nullptr, ys,
+                                      SlotGrid{0, nullptr, nullptr, nullptr}, stream);
+}
+
+hipError_t launch_w1_decode_slotgrid(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                                     const SlotGrid& sg, uint16_t* h, hipStream_t stream) {
+  if (!sg.active || !slot_grid_fits(sd.T, sd.top_k, sd.num_slots > sd.T * sd.top_k ? 1 : 0))
+    return hipErrorInvalidValue;
+  return launch_decode_picked<DEC_W1>(x, ed, sd, nullptr, nullptr, nullptr, 0, nullptr, h,
+                                      nullptr, sg, stream);
+}
+
+hipError_t launch_w2_decode_slotgrid(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                                     const SlotGrid& sg, float* ys, hipStream_t stream) {
+  if (!sg.active || sg.logits ||
+      !slot_grid_fits(sd.T, sd.top_k, sd.num_slots > sd.T * sd.top_k ? 1 : 0))
+    return hipErrorInvalidValue;
+  return launch_decode_picked<DEC_W2>(h, ed, sd, nullptr, nullptr, nullptr, 0, sg.weights, nullptr,
+                                      ys, sg, stream);
 }
 
 bool w2_token_sum_fits(const ExpertsDev& ed, const SlotsDev& sd) {

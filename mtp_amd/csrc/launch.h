@@ -38,6 +38,23 @@ hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int ha
                         int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp,
                         hipStream_t stream);
 
+// Slot-grid routing for decode-size batches (slot_grid_fits): the MFMA decode kernels take their
+// expert and rows from the routed ids themselves instead of an align pass. Workgroup y = slot
+// index; the workgroup at every 16th occurrence of an expert takes the next (up to) 16 slots of
+// that expert, the others leave. With `logits` (W1 of a layer call) every workgroup computes the
+// top-k of the (at most 8) tokens itself and workgroup (0, 0) publishes ids and weights; otherwise
+// they are read from `ids` / `weights`.
+struct SlotGrid {
+  int active;
+  const float* logits;  // [T][E+1] or nullptr
+  int32_t* ids;         // routed ids [T*top_k]
+  float* weights;       // routed weights [T*top_k] (+ T shared gates)
+};
+constexpr int kSlotGridMaxSlots = 64;  // all slots are the lanes of one wave
+inline bool slot_grid_fits(int T, int top_k, int has_shared) {
+  return topk_align_fits(T, top_k, has_shared);  // T <= 8, slots <= 64
+}
+
 // Decode path on MFMA with in-register dequantisation (blocks of kDecodeBlockM slots).
 hipError_t launch_w1_decode_mfma(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                                  const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
@@ -45,6 +62,10 @@ hipError_t launch_w1_decode_mfma(const uint16_t* x, const ExpertsDev& ed, const 
 hipError_t launch_w2_decode_mfma(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                  const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                                  int cap, const float* topk_w, float* ys, hipStream_t stream);
+hipError_t launch_w1_decode_slotgrid(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                                     const SlotGrid& sg, uint16_t* h, hipStream_t stream);
+hipError_t launch_w2_decode_slotgrid(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                                     const SlotGrid& sg, float* ys, hipStream_t stream);
 
 // Decode path on VALU dot products (v_dot2_f32_bf16) with shuffle K-reduction.
 hipError_t launch_w1_decode(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,

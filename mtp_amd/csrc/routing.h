@@ -165,6 +165,43 @@ MOE_DEV void topk_token(const float* __restrict__ row, int E, int top_k, int has
   }
 }
 
+// One wave: top-k of row[0..E) into LDS only (ids_lds[r], w_lds[r] for r < top_k), the same
+// selection and weights as topk_token.
+MOE_DEV void topk_token_lds(const float* __restrict__ row, int E, int top_k, int lane, int* ids_lds,
+                            float* w_lds) {
+  constexpr int MAXC = 8;
+  uint64_t key[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int e = lane + 64 * c;
+    key[c] = e < E ? topk_key(row[e], e) : 0ull;
+  }
+  float my_v = 0.0f;
+  int my_i = 0;
+  for (int r = 0; r < top_k; ++r) {
+    uint64_t head = 0;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) head = max_u64(head, key[c]);
+    const uint64_t best = wave_max_u64(head);
+    const int e = (int)(~(uint32_t)best);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+      if (key[c] == best) key[c] = 0ull;
+    if (lane == r) {
+      my_i = e;
+      my_v = row[e];
+    }
+  }
+  const float vmax = __shfl(my_v, 0, 64);
+  const float ex = (lane < top_k) ? expf(my_v - vmax) : 0.0f;
+  float s = 0.0f;
+  for (int r = 0; r < top_k; ++r) s = s + __shfl(ex, r, 64);
+  if (lane < top_k) {
+    ids_lds[lane] = my_i;
+    w_lds[lane] = ex / s;
+  }
+}
+
 // ---------------------------------------------------------------------------- align
 constexpr int kAlignWaves = 16;   // align_block needs blockDim.x == 1024
 constexpr int kMaxGroups = 513;   // 512 routed experts + the shared expert

@@ -183,3 +183,28 @@ def test_dropped_slots_contribute_zero(path, T):
     err = moe_ref.rel_err(got.float().cpu().numpy(), ref)
     _say(f"  rel_err={err:.3e}")
     assert np.isfinite(err) and err <= LAYER_RTOL
+
+
+@pytest.mark.parametrize("case", ["one_expert", "mixed"])
+def test_decode_repeated_ids(case):
+    """Caller-given ids may repeat an expert within and across tokens: at decode size the kernels
+    group slots per expert themselves (16 per workgroup), here with up to 64 slots of one expert."""
+    _say(f"repeated ids case={case}")
+    lay = small_layer(5)
+    g = to_gpu(lay)
+    T, k = 8, 8
+    rng = np.random.default_rng(55)
+    if case == "one_expert":
+        ids = np.full((T, k), 3, dtype=np.int32)
+    else:
+        ids = rng.choice([1, 2, 3, 9], size=(T, k)).astype(np.int32)
+    w = rng.uniform(0.05, 0.3, size=(T, k)).astype(np.float32)
+    x = synth.make_tokens(T, 512, seed=56)
+    ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(lay.experts))
+    for path in ("decode", "prefill", "gemv"):
+        got = ops.fused_experts(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
+                                g.experts, path=path)
+        torch.cuda.synchronize()
+        err = moe_ref.rel_err(got.float().cpu().numpy(), ref)
+        _say(f"  {path}: rel_err={err:.3e}")
+        assert np.isfinite(err) and err <= LAYER_RTOL
