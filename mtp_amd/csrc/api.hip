@@ -393,7 +393,9 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
                 "router logits");
   // decode-size batches: with one or two tokens the MFMA decode kernels compute the top-k
   // themselves (slot grid; every W1 workgroup repeats it, which costs more than the launch it
-  // saves beyond two tokens); otherwise top-k and align come from one block (no align launch)
+  // saves beyond two tokens); up to 8 tokens top-k and align come from one block (no align
+  // launch). Beyond that the selections are spread over many workgroups: one block would
+  // serialise them on one CU.
   const bool small = topk_align_fits(T, top_k, shared ? 1 : 0);
   Routing routing = ROUTE_ALIGN;
   if (path == MOE_PATH_DECODE && small && T <= kTokenSumMaxTokens) {

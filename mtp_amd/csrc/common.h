@@ -57,6 +57,37 @@ MOE_DEV uint32_t magic_pair(uint32_t w, int j) {
   return ((w >> (4 * j)) & 0x000F000Fu) | kMagicPair;
 }
 
+// Raw buffer loads (stride 0, unformatted). A byte offset at or past the resource's
+// num_records reads zeros without a memory access, so a lane whose data does not exist (a
+// padding row, a ring stage past the end of a slice) still issues the same instruction as the
+// others: every thread runs the same loads on every path and the compiler's wait counts stay
+// exact. Offsets in use stay below kOutOfRange; ORing kOutOfRange into one moves it out.
+constexpr int kBufferDword3 = 0x00020000;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+// Cache policy of a streamed-once load (nt).
+constexpr int kBufNontemporal = 2;
+
+// Resource over [base, base + num_bytes).
+MOE_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)num_bytes,
+                                           kBufferDword3);
+}
+// Resource over [base, base + 2 GiB) for data addressed by offsets below kOutOfRange.
+MOE_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) { return buf_rsrc(base, kOutOfRange); }
+
+template <int AUX = 0>
+MOE_DEV u32x4 buf_ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+}
+template <int AUX = 0>
+MOE_DEV u32x2 buf_ld64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX));
+}
+template <int AUX = 0>
+MOE_DEV uint32_t buf_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
+}
+
 MOE_DEV u32x4 ld128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 MOE_DEV u32x4 ld128_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

@@ -55,22 +55,6 @@ MOE_DEV bf16x8_v weight_frag(uint32_t w) {
   return as_frag(magic_pair(w, 0), magic_pair(w, 1), magic_pair(w, 2), magic_pair(w, 3));
 }
 
-// CT consecutive packed int32 of one qweight row (streamed once: nontemporal).
-template <int CT>
-MOE_DEV void load_packed(const int32_t* p, uint32_t (&w)[CT]) {
-  if constexpr (CT == 2) {
-    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-    w[0] = v[0];
-    w[1] = v[1];
-  } else {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    w[0] = v[0];
-    w[1] = v[1];
-    w[2] = v[2];
-    w[3] = v[3];
-  }
-}
-
 // Everything one lane needs for one quantisation group (SPG MFMA k-steps of 32).
 template <int NP, int SPG, int CT>
 struct GroupBuf {
@@ -80,44 +64,79 @@ struct GroupBuf {
   uint32_t z[NP];               // packed zeros word holding the CT columns
 };
 
-// One wave: acc[p*CT + j] += A[16 rows, k0 : k0+klen] . W_p[k0 : k0+klen, cl + j] for the NP
-// projections, klen a multiple of G. ap points at element (row of this lane, k0 + 8*kq);
-// valid_m = false makes this lane's A row zero. A ring of NB group buffers keeps groups
-// g + 1 .. g + NB - 1 in flight while group g is multiplied.
-template <int NP, int SPG, int CT, int NB>
-MOE_DEV void decode_tile(const ProjDev (&pj)[NP], const uint16_t* ap, bool valid_m, int NOUT,
-                         int G, int k0, int klen, int cl, int kq, f32x4 (&acc)[NP * CT]) {
-  constexpr int NT = NP * CT;
-  const int ngw = klen / G;
-  const int32_t* qp[NP];
-  const uint16_t* sp[NP];
-  const int32_t* zp[NP];
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    qp[p] = pj[p].qweight + (int64_t)(k0 / 8 + kq) * NOUT + cl;
-    sp[p] = pj[p].scales + (int64_t)(k0 / G) * NOUT + cl;
-    zp[p] = pj[p].qzeros + (int64_t)(k0 / G) * (NOUT / 8) + (cl >> 3);
-  }
-  const int zshift = 4 * (cl & 7);
+// A operand of one lane: resource over the activation rows and the byte offset of
+// (this lane's row, first k of the wave's slice + 8 * kq), kOutOfRange for a padding row.
+struct AView {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t off;
+};
 
-  auto load_group = [&](GroupBuf<NP, SPG, CT>& B, int gi) {
-    const int kg = gi * G;
+// One wave's view of a K slice [k0, k0 + NGW*G) of the NP projections at columns
+// cl .. cl + CT - 1. Every load is a buffer load from a uniform resource with a 32-bit lane
+// offset; group gi >= ngw (a ring stage past the slice) and padding rows load zeros with no
+// memory access, so the same instructions run on every path.
+template <int NP, int SPG, int CT>
+struct DecodeTile {
+  __amdgpu_buffer_rsrc_t qr[NP], sr[NP], zr[NP];
+  AView a;
+  uint32_t qoff, soff, zoff;        // lane offsets of group 0
+  uint32_t qgrp, sgrp, zgrp, qrow;  // bytes per group (qweight, scales, zeros), per packed row
+  int G, ngw, zshift;
+
+  MOE_DEV DecodeTile(const ProjDev (&pj)[NP], AView av, int NOUT, int G_, int k0, int klen,
+                     int cl, int kq)
+      : a(av), G(G_), ngw(klen / G_), zshift(4 * (cl & 7)) {
 #pragma unroll
-    for (int s = 0; s < SPG; ++s)
-      B.a[s] = valid_m ? ld128(ap + kg + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    for (int p = 0; p < NP; ++p) {
+      qr[p] = buf_rsrc(pj[p].qweight);
+      sr[p] = buf_rsrc(pj[p].scales);
+      zr[p] = buf_rsrc(pj[p].qzeros);
+    }
+    qrow = (uint32_t)NOUT * 4u;
+    qoff = (uint32_t)(k0 / 8 + kq) * qrow + (uint32_t)cl * 4u;
+    soff = (uint32_t)((k0 / G) * NOUT + cl) * 2u;
+    zoff = (uint32_t)((k0 / G) * (NOUT / 8) + (cl >> 3)) * 4u;
+    qgrp = (uint32_t)(G / 8) * qrow;
+    sgrp = (uint32_t)NOUT * 2u;
+    zgrp = (uint32_t)(NOUT / 8) * 4u;
+  }
+
+  MOE_DEV void load(GroupBuf<NP, SPG, CT>& B, int gi) const {
+    const uint32_t oob = gi < ngw ? 0u : kOutOfRange;
+    const uint32_t ug = (uint32_t)gi;
+#pragma unroll
+    for (int s = 0; s < SPG; ++s) B.a[s] = buf_ld128(a.r, (a.off + (ug * G + 32 * s) * 2u) | oob);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
 #pragma unroll
-      for (int s = 0; s < SPG; ++s) load_packed<CT>(qp[p] + (int64_t)(kg / 8 + 4 * s) * NOUT, B.w[p][s]);
-      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(sp[p] + (int64_t)gi * NOUT);
+      for (int s = 0; s < SPG; ++s) {  // weights are streamed once: nontemporal
+        const uint32_t o = (qoff + ug * qgrp + (uint32_t)(4 * s) * qrow) | oob;
+        if constexpr (CT == 2) {
+          const u32x2 v = buf_ld64<kBufNontemporal>(qr[p], o);
+          B.w[p][s][0] = v[0];
+          B.w[p][s][1] = v[1];
+        } else {
+          const u32x4 v = buf_ld128<kBufNontemporal>(qr[p], o);
 #pragma unroll
-      for (int j = 0; j < CT / 2; ++j) B.s[p][j] = s32[j];
-      B.z[p] = (uint32_t)zp[p][(int64_t)gi * (NOUT / 8)];  // shifted at use: no wait here
+          for (int j = 0; j < 4; ++j) B.w[p][s][j] = v[j];
+        }
+      }
+      if constexpr (CT == 2) {
+        B.s[p][0] = buf_ld32(sr[p], (soff + ug * sgrp) | oob);
+      } else {
+        const u32x2 v = buf_ld64(sr[p], (soff + ug * sgrp) | oob);
+        B.s[p][0] = v[0];
+        B.s[p][1] = v[1];
+      }
+      B.z[p] = buf_ld32(zr[p], (zoff + ug * zgrp) | oob);  // shifted at use: no wait here
     }
-  };
+  }
 
-  const bf16x8_v ones = as_frag(kOnes, kOnes, kOnes, kOnes);
-  auto compute_group = [&](const GroupBuf<NP, SPG, CT>& B) {
+  // acc[p*CT + j] += s * (sum_k x (128 + q) - (128 + z) * sum_k x) over one group. A group
+  // past the slice loaded zeros (scale 0) and adds +0.
+  MOE_DEV void compute(const GroupBuf<NP, SPG, CT>& B, f32x4 (&acc)[NP * CT]) const {
+    constexpr int NT = NP * CT;
+    const bf16x8_v ones = as_frag(kOnes, kOnes, kOnes, kOnes);
     f32x4 tmp[NT], tx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < NT; ++t) tmp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -125,13 +144,13 @@ MOE_DEV void decode_tile(const ProjDev (&pj)[NP], const uint16_t* ap, bool valid
     for (int s = 0; s < SPG; ++s) {
       uint32_t xp[4];
       xpairs(B.a[s], xp);
-      const bf16x8_v a = as_frag(xp[0], xp[1], xp[2], xp[3]);
-      tx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, tx, 0, 0, 0);
+      const bf16x8_v av = as_frag(xp[0], xp[1], xp[2], xp[3]);
+      tx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ones, tx, 0, 0, 0);
 #pragma unroll
       for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int j = 0; j < CT; ++j)
-          tmp[p * CT + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, weight_frag(B.w[p][s][j]),
+          tmp[p * CT + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, weight_frag(B.w[p][s][j]),
                                                                     tmp[p * CT + j], 0, 0, 0);
     }
 #pragma unroll
@@ -146,20 +165,26 @@ MOE_DEV void decode_tile(const ProjDev (&pj)[NP], const uint16_t* ap, bool valid
           acc[p * CT + j][i] =
               __builtin_fmaf(sc, __builtin_fmaf(-zb, tx[i], tmp[p * CT + j][i]), acc[p * CT + j][i]);
       }
-  };
+  }
+};
 
+// One wave: acc[p*CT + j] += A[16 rows, k0 : k0+klen] . W_p[k0 : k0+klen, cl + j] for the NP
+// projections, klen a multiple of G. A ring of NB group buffers keeps groups g + 1 .. g + NB - 1
+// in flight while group g is multiplied; the loop body issues the same loads on every pass
+// (stages past the slice read zeros), so each wait is for exactly the group about to be used.
+template <int NP, int SPG, int CT, int NB>
+MOE_DEV void decode_tile(const DecodeTile<NP, SPG, CT>& tile, f32x4 (&acc)[NP * CT]) {
   GroupBuf<NP, SPG, CT> ring[NB];
 #pragma unroll
-  for (int j = 0; j < NB - 1; ++j)
-    if (j < ngw) load_group(ring[j], j);
-  for (int g0 = 0; g0 < ngw; g0 += NB) {
+  for (int j = 0; j < NB - 1; ++j) tile.load(ring[j], j);
+  for (int g0 = 0; g0 < tile.ngw; g0 += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int g = g0 + j;
-      if (g < ngw) {
-        if (g + NB - 1 < ngw) load_group(ring[(j + NB - 1) % NB], g + NB - 1);
-        compute_group(ring[j]);
-      }
+      tile.load(ring[(j + NB - 1) % NB], g0 + j + NB - 1);
+      // keep the stage's loads ahead of the wait for group g0 + j (the scheduler would sink
+      // them below it, leaving one group in flight)
+      __builtin_amdgcn_sched_barrier(0);
+      tile.compute(ring[j], acc);
     }
   }
 }
@@ -173,74 +198,14 @@ MOE_DEV void static_for(F&& f) {
   }
 }
 
-// decode_tile for a K range of exactly NGW groups with every load issued up front (straight-line
-// code: the compiler's per-register waits let group g be multiplied as soon as it has landed
-// while the later groups are still in flight).
+// decode_tile for a K slice of exactly NGW groups with every load issued up front (straight-line
+// code: group g is multiplied as soon as it has landed while the later groups are in flight).
 template <int NP, int SPG, int CT, int NGW>
-MOE_DEV void decode_tile_fixed(const ProjDev (&pj)[NP], const uint16_t* ap, bool valid_m,
-                               int NOUT, int G, int k0, int cl, int kq, f32x4 (&acc)[NP * CT]) {
-  constexpr int NT = NP * CT;
-  // uniform bases + one 32-bit per-lane offset per stream (scalar-base loads)
-  const uint32_t qoff = (uint32_t)(((int64_t)kq * NOUT + cl) * 4);
-  const uint32_t soff = (uint32_t)(cl * 2);
-  const uint32_t zoff = (uint32_t)((cl >> 3) * 4);
-  const int zshift = 4 * (cl & 7);
+MOE_DEV void decode_tile_fixed(const DecodeTile<NP, SPG, CT>& tile, f32x4 (&acc)[NP * CT]) {
   GroupBuf<NP, SPG, CT> ring[NGW];
-  static_for<0, NGW>([&](auto gc) {
-    constexpr int gi = gc.value;
-    GroupBuf<NP, SPG, CT>& B = ring[gi];
-    const int kg = gi * G;
-#pragma unroll
-    for (int s = 0; s < SPG; ++s)
-      B.a[s] = valid_m ? ld128(ap + kg + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const char* qg = reinterpret_cast<const char*>(pj[p].qweight) +
-                       (int64_t)((k0 + kg) / 8) * NOUT * 4;
-#pragma unroll
-      for (int s = 0; s < SPG; ++s)
-        load_packed<CT>(reinterpret_cast<const int32_t*>(qg + (int64_t)(4 * s) * NOUT * 4 + qoff),
-                        B.w[p][s]);
-      const int g = (k0 + kg) / G;
-      const char* sg = reinterpret_cast<const char*>(pj[p].scales) + (int64_t)g * NOUT * 2 + soff;
-#pragma unroll
-      for (int j = 0; j < CT / 2; ++j) B.s[p][j] = reinterpret_cast<const uint32_t*>(sg)[j];
-      B.z[p] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(pj[p].qzeros) +
-                                                  (int64_t)g * (NOUT / 8) * 4 + zoff);
-    }
-  });
-  const bf16x8_v ones = as_frag(kOnes, kOnes, kOnes, kOnes);
-  static_for<0, NGW>([&](auto gc) {
-    const GroupBuf<NP, SPG, CT>& B = ring[gc.value];
-    f32x4 tmp[NT], tx = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < NT; ++t) tmp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < SPG; ++s) {
-      uint32_t xp[4];
-      xpairs(B.a[s], xp);
-      const bf16x8_v a = as_frag(xp[0], xp[1], xp[2], xp[3]);
-      tx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, tx, 0, 0, 0);
-#pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int j = 0; j < CT; ++j)
-          tmp[p * CT + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, weight_frag(B.w[p][s][j]),
-                                                                    tmp[p * CT + j], 0, 0, 0);
-    }
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int j = 0; j < CT; ++j) {
-        const uint32_t s2 = B.s[p][j >> 1];
-        const float sc = f16_to_f32((j & 1) ? (s2 >> 16) : (s2 & 0xFFFFu));
-        const float zb = kMagicBias + (float)((B.z[p] >> (zshift + 4 * j)) & 0xFu);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[p * CT + j][i] =
-              __builtin_fmaf(sc, __builtin_fmaf(-zb, tx[i], tmp[p * CT + j][i]), acc[p * CT + j][i]);
-      }
-  });
+  static_for<0, NGW>([&](auto gc) { tile.load(ring[gc.value], gc.value); });
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+  static_for<0, NGW>([&](auto gc) { tile.compute(ring[gc.value], acc); });
 }
 
 MOE_DEV void projections(const ExpertsDev& ed, int mode, bool is_shared, ProjDev* pj) {
@@ -265,7 +230,8 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
   constexpr int TW = 16 * CT;                    // columns per block
   __shared__ float red[(KS > 1 ? KS - 1 : 1) * NT * 4 * 64];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar K-slice offsets
   int e, f_m, f_out[4];  // expert; A row of this lane; D rows of this lane
   if (sg.active) {
     // Slot grid (SlotGrid in launch.h): slots from the routed ids, no align pass.
@@ -276,8 +242,11 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
     if (sg.logits) {  // every workgroup computes the same top-k of the (at most 8) tokens
       for (int t = wave; t < sd.T; t += KS) {
         const float* row = sg.logits + (int64_t)t * (E + 1);
-        topk_token_lds(row, E, sd.top_k, lane, s_ids + t * sd.top_k, s_w + t * sd.top_k);
-        if (n_slots > routed && lane == 0) s_w[routed + t] = 1.0f / (1.0f + expf(-row[E]));
+        const bool shared = n_slots > routed;  // row[E] is the shared gate's logit
+        const float g = __uint_as_float(
+            buf_ld32(buf_rsrc(row, (uint32_t)(E + (shared ? 1 : 0)) * 4u), (uint32_t)E * 4u));
+        topk_token_lds_any(row, E, sd.top_k, lane, s_ids + t * sd.top_k, s_w + t * sd.top_k);
+        if (shared && lane == 0) s_w[routed + t] = 1.0f / (1.0f + expf(-g));
       }
     } else if (tid < routed) {
       s_ids[tid] = sg.ids[tid];
@@ -331,18 +300,20 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
   const int kw0 = wave * kslice;
   const int m = lane & 15, kq = lane >> 4;
   const bool valid_m = (unsigned)f_m < (unsigned)sd.num_slots;
-  const int64_t arow = valid_m ? ((MODE == DEC_W1) ? (int64_t)slot_token(sd, f_m) : (int64_t)f_m) : 0;
+  const uint32_t arow = valid_m ? ((MODE == DEC_W1) ? (uint32_t)slot_token(sd, f_m) : (uint32_t)f_m) : 0u;
+  const uint32_t a_rows = (MODE == DEC_W1) ? (uint32_t)sd.T : (uint32_t)sd.num_slots;
+  const AView av{buf_rsrc(act, a_rows * (uint32_t)K * 2u),
+                 valid_m ? (arow * (uint32_t)K + (uint32_t)(kw0 + 8 * kq)) * 2u : kOutOfRange};
   const int cl = blockIdx.x * TW + CT * m;  // this lane's first column
+  const DecodeTile<NP, SPG, CT> tile(pj, av, NOUT, G, kw0, kslice, cl, kq);
 
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   if constexpr (NB < 0) {  // fixed: the wave's slice is exactly -NB groups, all loads up front
-    decode_tile_fixed<NP, SPG, CT, -NB>(pj, act + arow * K + kw0 + 8 * kq, valid_m, NOUT, G, kw0,
-                                        cl, kq, acc);
+    decode_tile_fixed<NP, SPG, CT, -NB>(tile, acc);
   } else {
-    decode_tile<NP, SPG, CT, NB>(pj, act + arow * K + kw0 + 8 * kq, valid_m, NOUT, G, kw0, kslice,
-                                 cl, kq, acc);
+    decode_tile<NP, SPG, CT, NB>(tile, acc);
   }
 
   if constexpr (KS > 1) {  // cross-wave reduction: waves 1.. write, wave 0 sums in wave order
@@ -402,7 +373,9 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
   constexpr int TW = 16 * CT;
   __shared__ float part[kTokenSumMaxWaves][TW];
   const int t = blockIdx.y;
-  const int lane = threadIdx.x & 63, i = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int i = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // uniform: the slot's
+                                                                         // resources in SGPRs
   const int nwaves = blockDim.x >> 6;
   const bool is_shared = i >= sd.top_k;
   const int f = is_shared ? sd.T * sd.top_k + t : t * sd.top_k + i;
@@ -420,8 +393,14 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
     ProjDev pj[1];
     projections(ed, DEC_W2, is_shared, pj);
     pj[0] = proj_row(pj[0], is_shared ? 0 : ed.row_stride, row, K / 8, K / G, NOUT);
-    decode_tile<1, SPG, CT, NB>(pj, h + (int64_t)f * K + 8 * kq, m == 0, NOUT, G, 0, K, cl, kq,
-                                acc);
+    const AView av{buf_rsrc(h, (uint32_t)sd.num_slots * (uint32_t)K * 2u),
+                   m == 0 ? ((uint32_t)f * (uint32_t)K + (uint32_t)(8 * kq)) * 2u : kOutOfRange};
+    const DecodeTile<1, SPG, CT> tile(pj, av, NOUT, G, 0, K, cl, kq);
+    if constexpr (NB < 0) {  // K is exactly -NB groups: every load up front
+      decode_tile_fixed<1, SPG, CT, -NB>(tile, acc);
+    } else {
+      decode_tile<1, SPG, CT, NB>(tile, acc);
+    }
   }
   const float w = ok ? topk_w[f] : 0.0f;
   if (lane < 16) {  // row 0 of the tile: lanes 0..15, element 0
@@ -437,12 +416,21 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
   }
 }
 
+// Every buffer offset the decode kernels form (activation rows, one expert's qweight, scales
+// and zeros) stays below kOutOfRange.
+bool decode_offsets_fit(const ExpertsDev& ed, const SlotsDev& sd) {
+  const int64_t lim = kOutOfRange;
+  return (int64_t)sd.T * ed.hidden * 2 < lim && (int64_t)sd.num_slots * ed.inter * 2 < lim &&
+         (int64_t)ed.hidden * ed.inter / 2 < lim;
+}
+
 template <int MODE, int SPG, int KS, int CT, int NB>
 hipError_t launch_cfg(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int cap,
                       const float* topk_w, uint16_t* h, float* ys, const SlotGrid& sg,
                       hipStream_t stream) {
   const int NOUT = (MODE == DEC_W1) ? ed.inter : ed.hidden;
+  if (!decode_offsets_fit(ed, sd)) return hipErrorInvalidValue;
   const dim3 grid(NOUT / (16 * CT), sg.active ? sd.num_slots : cap);
   hipLaunchKernelGGL((gemm_decode_kernel<MODE, SPG, KS, CT, NB>), grid, dim3(64 * KS), 0, stream,
                      act, ed, sd, sorted, eids, ntpp, topk_w, h, ys, sg);
@@ -479,8 +467,6 @@ hipError_t launch_decode_cfg(const uint16_t* act, const ExpertsDev& ed, const Sl
                                              ys, sg, stream);
   MOE_DEC_CASE(1, 2, 2) MOE_DEC_CASE(2, 2, 2) MOE_DEC_CASE(4, 2, 2) MOE_DEC_CASE(8, 2, 2)
   MOE_DEC_CASE(1, 4, 2) MOE_DEC_CASE(2, 4, 2) MOE_DEC_CASE(4, 4, 2)
-  MOE_DEC_CASE(1, 2, 3) MOE_DEC_CASE(2, 2, 3) MOE_DEC_CASE(4, 2, 3)
-  MOE_DEC_CASE(1, 4, 3) MOE_DEC_CASE(2, 4, 3)
   // fixed slices (nb = -groups per wave), all loads in flight at once
   MOE_DEC_CASE(1, 2, -4) MOE_DEC_CASE(2, 2, -4) MOE_DEC_CASE(4, 2, -4) MOE_DEC_CASE(8, 2, -2)
   MOE_DEC_CASE(1, 4, -4) MOE_DEC_CASE(2, 4, -4) MOE_DEC_CASE(4, 4, -4) MOE_DEC_CASE(8, 4, -2)
@@ -491,34 +477,41 @@ hipError_t launch_decode_cfg(const uint16_t* act, const ExpertsDev& ed, const Sl
 }
 
 // Configuration by problem size (measured on MI355X, 40 Zipf-skewed layers of H 2048, I 512,
-// E 256, top-8): few active expert blocks -> split K over more waves with every load of a wave
-// issued up front; many -> two waves per block with a double-buffered ring. W2 (K = 512) uses
-// four columns per lane: its 16-slot activation fragment is then shared by more columns.
+// E 256, top-8, group 128; num_slots 8 / 64 / 256 / 512 at batch 1 / 8 / 32 / 64):
+//   W1: up to 16 slots, 8 waves over K with both of a wave's groups loaded up front (7.2 us);
+//       up to 128, four waves over K with a 2-deep ring (14.4 us); up to 384, two waves (24.0 us);
+//       beyond, four waves and four columns per lane (33.1 us).
+//   W2 (K = 512, four columns per lane): two waves over K with both groups up front, except
+//       between 128 and 384 slots where one wave with a 2-deep ring is faster (12.9 vs 13.4 us).
 template <int MODE>
 void pick_decode_cfg(const ExpertsDev& ed, const SlotsDev& sd, int* ks, int* ct, int* nb) {
   const int K = (MODE == DEC_W1) ? ed.hidden : ed.inter;
   const int groups = K / ed.group;
-  const int blocks_est = sd.num_slots < ed.num_experts ? sd.num_slots : ed.num_experts;
+  const int slots = sd.num_slots;
   auto fixed = [&](int k) {  // k waves over K, all of a wave's groups in flight
-    if (groups % k == 0 && (groups / k == 4 || groups / k == 2)) {
+    if (k >= 1 && groups % k == 0 && (groups / k == 4 || groups / k == 2)) {
       *ks = k;
       *nb = -(groups / k);
       return true;
     }
     return false;
   };
-  if (MODE == DEC_W1) {
-    *ct = 2;
-    if (blocks_est < 96 && fixed(groups / 4)) return;
-    *ks = 2;
+  auto ring = [&](int k) {  // k waves over K (fewer when K does not split), 2-deep ring
+    *ks = k;
     *nb = 2;
     while (*ks > 1 && K % (*ks * ed.group) != 0) *ks /= 2;
-    return;
+  };
+  if (MODE == DEC_W1) {
+    *ct = 2;
+    if (slots <= 16 && fixed(groups / 2)) return;
+    if (slots <= 128) return ring(4);
+    if (slots <= 384) return ring(2);
+    *ct = ed.inter % 64 == 0 ? 4 : 2;
+    return ring(4);
   }
   *ct = ed.hidden % 64 == 0 ? 4 : 2;
-  if (blocks_est < 96 && fixed(groups / 2)) return;
-  *ks = 1;
-  *nb = 2;
+  if ((slots <= 128 || slots > 384) && fixed(groups / 2)) return;
+  ring(1);
 }
 
 template <int SPG, int CT, int NB>
@@ -591,11 +584,18 @@ bool w2_token_sum_fits(const ExpertsDev& ed, const SlotsDev& sd) {
 hipError_t launch_w2_token_sum(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                const int32_t* ids, const float* topk_w, uint16_t* out,
                                hipStream_t stream) {
-  if (!w2_token_sum_fits(ed, sd)) return hipErrorInvalidValue;
-  switch (ed.group) {  // ring depth: all groups of K = 512 in flight at once
-    case 64: return launch_token_sum<2, 2, 8>(h, ed, sd, ids, topk_w, out, stream);
-    case 128: return launch_token_sum<4, 2, 4>(h, ed, sd, ids, topk_w, out, stream);
-    case 256: return launch_token_sum<8, 2, 2>(h, ed, sd, ids, topk_w, out, stream);
+  if (!w2_token_sum_fits(ed, sd) || !decode_offsets_fit(ed, sd)) return hipErrorInvalidValue;
+  const int groups = ed.inter / ed.group;
+  switch (ed.group) {  // K = 512: all of a slot's groups in flight at once; else a 2-deep ring
+    case 64:
+      return groups == 8 ? launch_token_sum<2, 2, -8>(h, ed, sd, ids, topk_w, out, stream)
+                         : launch_token_sum<2, 2, 2>(h, ed, sd, ids, topk_w, out, stream);
+    case 128:
+      return groups == 4 ? launch_token_sum<4, 2, -4>(h, ed, sd, ids, topk_w, out, stream)
+                         : launch_token_sum<4, 2, 2>(h, ed, sd, ids, topk_w, out, stream);
+    case 256:
+      return groups == 2 ? launch_token_sum<8, 2, -2>(h, ed, sd, ids, topk_w, out, stream)
+                         : launch_token_sum<8, 2, 2>(h, ed, sd, ids, topk_w, out, stream);
     default: return hipErrorInvalidValue;
   }
 }

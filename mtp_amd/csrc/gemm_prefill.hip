@@ -30,10 +30,6 @@ constexpr int LDS_STRIDE = BK + 8;  // bf16 per LDS row (16 B padding against ba
 constexpr int kMTiles = BM / 16;    // 8 row subtiles
 constexpr int kAChunks = BM * BK / 8 / 256;  // 16-byte A chunks per thread and step (8)
 
-// Buffer-resource word 3 for raw (unformatted, stride 0) buffers on gfx9; a byte offset at or
-// past num_records reads zeros without touching memory.
-constexpr int kBufferDword3 = 0x00020000;
-constexpr uint32_t kOutOfRange = 0x80000000u;
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));

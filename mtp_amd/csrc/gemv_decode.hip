@@ -225,6 +225,11 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(const uint16_t* __rest
 // ------------------------------------------------------------------------------- moe_sum
 // out[t] = bf16(sum over the token's slots in order of ys[slot]). With `ids`, routed slots whose
 // expert is dropped (routed_ok false: their ys rows were never written) are skipped.
+// Slots are taken TK at a time: all loads of a chunk are issued together as buffer loads (a
+// skipped slot or one past top_k reads zeros without a memory access, and +0 leaves the running
+// sum unchanged), so a chunk waits for three memory latencies (ids, expert_row, ys) instead of
+// one per slot. The sum runs over the slots in order.
+template <int TK>
 __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ ys, int T,
                                                       int top_k, int H, int has_shared,
                                                       const int32_t* __restrict__ ids,
@@ -233,20 +238,49 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ 
                                                       uint16_t* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int per_row = H / 4;
-  const int64_t t = idx / per_row;
+  const int t = (int)(idx / per_row);
   if (t >= T) return;
   const int c = (int)(idx % per_row) * 4;
+  const int routed = T * top_k;
+  const __amdgpu_buffer_rsrc_t yr =
+      buf_rsrc(ys, (uint32_t)(routed + (has_shared ? T : 0)) * (uint32_t)H * 4u);
+  const __amdgpu_buffer_rsrc_t ir = buf_rsrc(ids, ids ? (uint32_t)routed * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t er = buf_rsrc(expert_row, expert_row ? (uint32_t)num_experts * 4u : 0u);
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < top_k; ++i) {
-    const int64_t f = t * top_k + i;
-    if (ids && !routed_ok(expert_row, num_experts, ids[f])) continue;
-    s += *reinterpret_cast<const f32x4*>(ys + f * H + c);
+  for (int i0 = 0; i0 < top_k; i0 += TK) {
+    bool ok[TK];
+#pragma unroll
+    for (int i = 0; i < TK; ++i) ok[i] = i0 + i < top_k;
+    if (ids) {
+      int e[TK];
+#pragma unroll
+      for (int i = 0; i < TK; ++i)
+        e[i] = (int)buf_ld32(ir, ok[i] ? (uint32_t)(t * top_k + i0 + i) * 4u : kOutOfRange);
+#pragma unroll
+      for (int i = 0; i < TK; ++i) ok[i] = ok[i] && e[i] >= 0 && e[i] < num_experts;
+      if (expert_row) {
+        int r[TK];
+#pragma unroll
+        for (int i = 0; i < TK; ++i) r[i] = (int)buf_ld32(er, ok[i] ? (uint32_t)e[i] * 4u : kOutOfRange);
+#pragma unroll
+        for (int i = 0; i < TK; ++i) ok[i] = ok[i] && r[i] >= 0;
+      }
+    }
+    f32x4 v[TK];
+#pragma unroll
+    for (int i = 0; i < TK; ++i)
+      v[i] = __builtin_bit_cast(
+          f32x4, buf_ld128(yr, ok[i] ? ((uint32_t)(t * top_k + i0 + i) * (uint32_t)H + (uint32_t)c) * 4u
+                                     : kOutOfRange));
+#pragma unroll
+    for (int i = 0; i < TK; ++i) s += v[i];
   }
-  if (has_shared) s += *reinterpret_cast<const f32x4*>(ys + ((int64_t)T * top_k + t) * H + c);
+  if (has_shared)
+    s += __builtin_bit_cast(f32x4, buf_ld128(yr, ((uint32_t)(routed + t) * (uint32_t)H + (uint32_t)c) * 4u));
   u32x2 o;
   o[0] = pack_bf16x2(s[0], s[1]);
   o[1] = pack_bf16x2(s[2], s[3]);
-  *reinterpret_cast<u32x2*>(out + t * H + c) = o;
+  *reinterpret_cast<u32x2*>(out + (int64_t)t * H + c) = o;
 }
 
 }  // namespace
@@ -277,7 +311,17 @@ hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shar
                           uint16_t* out, hipStream_t stream) {
   const int64_t n = (int64_t)T * (H / 4);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(moe_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ys,
-                     T, top_k, H, has_shared, ids, num_experts, expert_row, out);
+  if ((int64_t)(T * top_k + T) * H * 4 >= kOutOfRange) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((n + 255) / 256));
+#define MOE_SUM_CASE(TKV)                                                                     \
+  if (top_k <= TKV) {                                                                         \
+    hipLaunchKernelGGL(moe_sum_kernel<TKV>, grid, dim3(256), 0, stream, ys, T, top_k, H,       \
+                       has_shared, ids, num_experts, expert_row, out);                        \
+    return hipGetLastError();                                                                 \
+  }
+  MOE_SUM_CASE(1) MOE_SUM_CASE(2) MOE_SUM_CASE(4) MOE_SUM_CASE(8)
+#undef MOE_SUM_CASE
+  hipLaunchKernelGGL(moe_sum_kernel<16>, grid, dim3(256), 0, stream, ys, T, top_k, H, has_shared,
+                     ids, num_experts, expert_row, out);
   return hipGetLastError();
 }

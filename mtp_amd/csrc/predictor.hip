@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256) void mlp_logits_kernel(
     const uint16_t* __restrict__ x, int64_t x_head, int T, int K, const uint16_t* __restrict__ W,
     int64_t w_head, int N, float* __restrict__ out, int64_t out_head) {
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int wave = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tiles_n = (N + TE - 1) / TE;
   const int t0 = (wave / tiles_n) * TT;
   const int n0 = (wave % tiles_n) * TE;
@@ -48,11 +48,11 @@ __global__ __launch_bounds__(256) void predictor_topk_kernel(const float* __rest
                                                              int32_t* __restrict__ ids,
                                                              float* __restrict__ scores) {
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int w = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (w >= T * L) return;
   const int l = w / T, t = w % T;
   const int64_t head_off = (int64_t)l * T * top_k;
-  topk_token(logits + (int64_t)w * (E + 1), E, top_k, 0, T, t, lane, ids + head_off,
+  topk_token_any(logits + (int64_t)w * (E + 1), E, top_k, 0, T, t, lane, ids + head_off,
              scores + head_off, nullptr);
 }
 

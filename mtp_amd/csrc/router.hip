@@ -24,7 +24,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     float* __restrict__ logits) {
   const int rows = E + (shared_w ? 1 : 0);
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int wave = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tiles_e = (rows + TE - 1) / TE;
   const int t0 = (wave / tiles_e) * TT;
   const int e0 = (wave % tiles_e) * TE;
@@ -172,9 +172,9 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
                                                           int32_t* __restrict__ ids,
                                                           float* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int t = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= T) return;
-  topk_token(logits + (int64_t)t * (E + 1), E, top_k, has_shared, T, t, lane, ids, weights,
+  topk_token_any(logits + (int64_t)t * (E + 1), E, top_k, has_shared, T, t, lane, ids, weights,
              nullptr);
 }
 
@@ -184,9 +184,9 @@ __global__ __launch_bounds__(64 * kTopkAlignMaxTokens) void topk_align_kernel(
     int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ sorted,
     int32_t* __restrict__ eids, int32_t* __restrict__ ntpp) {
   __shared__ int s_ids[kAlignWaveMaxSlots];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave < T)
-    topk_token(logits + (int64_t)wave * (E + 1), E, top_k, has_shared, T, wave, lane, ids,
+    topk_token_any(logits + (int64_t)wave * (E + 1), E, top_k, has_shared, T, wave, lane, ids,
                weights, s_ids);
   __syncthreads();
   if (wave == 0) align_wave(s_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, lane);

@@ -21,41 +21,59 @@ MOE_DEV void logits_tile(const uint16_t* __restrict__ x, int T, int H, const uin
                          int E, const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
                          float* __restrict__ logits, int t0, int e0, int lane) {
   const int rows = E + (shared_w ? 1 : 0);
-  const uint16_t* wrow[TE];
+  // Buffer loads: a token or router row outside the tile's range, and chunks past H, read zeros
+  // without a memory access, so every iteration issues the same loads (exact wait counts).
+  // t0 and e0 are wave-uniform: the resources and row offsets live in scalar registers.
+  const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, (uint32_t)T * (uint32_t)H * 2u);
+  const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W, (uint32_t)E * (uint32_t)H * 2u);
+  const __amdgpu_buffer_rsrc_t sr = buf_rsrc(shared_w, shared_w ? (uint32_t)H * 2u : 0u);
+  uint32_t xo[TT], wo[TE];
+#pragma unroll
+  for (int i = 0; i < TT; ++i) xo[i] = (t0 + i < T) ? (uint32_t)(t0 + i) * (uint32_t)H * 2u : kOutOfRange;
 #pragma unroll
   for (int j = 0; j < TE; ++j) {
     const int e = e0 + j;
-    wrow[j] = e < E ? W + (int64_t)e * H : (e == E && shared_w ? shared_w : nullptr);
+    wo[j] = e < E ? (uint32_t)e * (uint32_t)H * 2u : (e == E && shared_w ? 0u : kOutOfRange);
   }
-  const uint16_t* xrow[TT];
-#pragma unroll
-  for (int i = 0; i < TT; ++i) xrow[i] = (t0 + i < T) ? x + (int64_t)(t0 + i) * H : nullptr;
   float acc[TT][TE];
 #pragma unroll
   for (int i = 0; i < TT; ++i)
 #pragma unroll
     for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
 
+  // Lane l owns chunks q = l, l + 64, ... (8 bf16 each) and accumulates them in increasing q;
+  // NI iterations of loads are in flight before their arithmetic.
+  constexpr int NI = 4;
   const int nq = H / 8;
-#pragma unroll 4
-  for (int q = lane; q < nq; q += 64) {
-    u32x4 xv[TT], wv[TE];
+  for (int q0 = 0; q0 < nq; q0 += 64 * NI) {
+    u32x4 xv[NI][TT], wv[NI][TE];
 #pragma unroll
-    for (int i = 0; i < TT; ++i) xv[i] = xrow[i] ? ld128(xrow[i] + 8 * q) : u32x4{0, 0, 0, 0};
+    for (int it = 0; it < NI; ++it) {
+      const int q = q0 + 64 * it + lane;
+      const uint32_t qo = q < nq ? (uint32_t)q * 16u : kOutOfRange;
 #pragma unroll
-    for (int j = 0; j < TE; ++j) wv[j] = wrow[j] ? ld128(wrow[j] + 8 * q) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int el = 0; el < 8; ++el) {
-      float wf[TE];
+      for (int i = 0; i < TT; ++i) xv[it][i] = buf_ld128(xr, (xo[i] + qo) | (qo & kOutOfRange));
 #pragma unroll
       for (int j = 0; j < TE; ++j)
-        wf[j] = (el & 1) ? bf16hi_to_f32(wv[j][el >> 1]) : bf16lo_to_f32(wv[j][el >> 1]);
+        wv[it][j] = buf_ld128(e0 + j == E ? sr : wr, (wo[j] + qo) | (qo & kOutOfRange));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the NI iterations before the first wait
 #pragma unroll
-      for (int i = 0; i < TT; ++i) {
-        const uint32_t xd = xv[i][el >> 1];
-        const float xf = (el & 1) ? bf16hi_to_f32(xd) : bf16lo_to_f32(xd);
+    for (int it = 0; it < NI; ++it) {
+      if (q0 + 64 * it + lane >= nq) continue;  // no arithmetic past H (keeps the fma chain exact)
 #pragma unroll
-        for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xf, wf[j], acc[i][j]);
+      for (int el = 0; el < 8; ++el) {
+        float wf[TE];
+#pragma unroll
+        for (int j = 0; j < TE; ++j)
+          wf[j] = (el & 1) ? bf16hi_to_f32(wv[it][j][el >> 1]) : bf16lo_to_f32(wv[it][j][el >> 1]);
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+          const uint32_t xd = xv[it][i][el >> 1];
+          const float xf = (el & 1) ? bf16hi_to_f32(xd) : bf16lo_to_f32(xd);
+#pragma unroll
+          for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xf, wf[j], acc[i][j]);
+        }
       }
     }
   }
@@ -88,118 +106,138 @@ MOE_DEV void logits_tile(const uint16_t* __restrict__ x, int T, int H, const uin
 }
 
 // ---------------------------------------------------------------------------- top-k
-// Total order on (logit, expert): larger logit first, then lower id. NaN ranks last.
-MOE_DEV uint64_t topk_key(float v, int e) {
+// 32-bit order key of a logit: unsigned order = logit order, with -0 equal to +0 and NaN (key 1)
+// below every number; key 0 marks "not a candidate" (already selected, or past E).
+MOE_DEV uint32_t topk_ord(float v) {
   uint32_t u = __float_as_uint(v);
+  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;  // -0 -> +0
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  if ((__float_as_uint(v) & 0x7FFFFFFFu) > 0x7F800000u) u = 0;
-  return ((uint64_t)u << 32) | (uint32_t)(~(uint32_t)e);
+  return ((__float_as_uint(v) & 0x7FFFFFFFu) > 0x7F800000u) ? 1u : u;
 }
 
-MOE_DEV uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// The logit of a key (a NaN for key 1; +0 for either zero).
+MOE_DEV float topk_ord_value(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
 
+// DPP move with 0 in the lanes a row mask leaves out (0 is the identity of unsigned max, so the
+// move and the max fuse into one v_max_u32_dpp).
 #define MOE_DPP(v, ctrl, rmask) \
-  (uint32_t) __builtin_amdgcn_update_dpp((int)(v), (int)(v), ctrl, rmask, 0xF, false)
+  (uint32_t) __builtin_amdgcn_update_dpp(0, (int)(v), ctrl, rmask, 0xF, false)
 
-// Wave-wide maximum of a 64-bit key through DPP (quad xor 1, quad xor 2, half-row mirror, row
-// mirror, row_bcast15, row_bcast31); the result is read from lane 63 and is wave-uniform.
-MOE_DEV uint64_t wave_max_u64(uint64_t v) {
-#define MOE_DPP_STEP(ctrl, rmask)                                  \
-  do {                                                             \
-    const uint32_t lo_ = MOE_DPP((uint32_t)v, ctrl, rmask);        \
-    const uint32_t hi_ = MOE_DPP((uint32_t)(v >> 32), ctrl, rmask); \
-    v = max_u64(v, ((uint64_t)hi_ << 32) | lo_);                   \
-  } while (0)
-  MOE_DPP_STEP(0xB1, 0xF);   // quad_perm(1,0,3,2)
-  MOE_DPP_STEP(0x4E, 0xF);   // quad_perm(2,3,0,1)
-  MOE_DPP_STEP(0x141, 0xF);  // row_half_mirror
-  MOE_DPP_STEP(0x140, 0xF);  // row_mirror
-  MOE_DPP_STEP(0x142, 0xA);  // row_bcast15 into rows 1, 3
-  MOE_DPP_STEP(0x143, 0xC);  // row_bcast31 into rows 2, 3
-#undef MOE_DPP_STEP
-  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-  return ((uint64_t)hi << 32) | lo;
+// Wave-wide maximum through DPP (quad xor 1, quad xor 2, half-row mirror, row mirror,
+// row_bcast15, row_bcast31); the result is read from lane 63 and is wave-uniform.
+MOE_DEV uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, MOE_DPP(v, 0xB1, 0xF));   // quad_perm(1,0,3,2)
+  v = max(v, MOE_DPP(v, 0x4E, 0xF));   // quad_perm(2,3,0,1)
+  v = max(v, MOE_DPP(v, 0x141, 0xF));  // row_half_mirror
+  v = max(v, MOE_DPP(v, 0x140, 0xF));  // row_mirror
+  v = max(v, MOE_DPP(v, 0x142, 0xA));  // row_bcast15 into rows 1, 3
+  v = max(v, MOE_DPP(v, 0x143, 0xC));  // row_bcast31 into rows 2, 3
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// One wave: top-k of row[0..E) (E <= 512). Writes ids[t*k + r], weights[t*k + r] (r < k) and,
-// when has_shared, weights[T*k + t] = sigmoid(row[E]). Optionally mirrors the ids to ids_lds.
-MOE_DEV void topk_token(const float* __restrict__ row, int E, int top_k, int has_shared, int T,
-                        int t, int lane, int32_t* __restrict__ ids, float* __restrict__ weights,
-                        int* ids_lds) {
-  constexpr int MAXC = 8;
-  uint64_t key[MAXC];
+// One wave: the top_k (<= 64) largest of row[0..E) (E <= 64 * MAXC), larger logit first and
+// equal logits by lower id (the reference's tie rule made explicit). Lane r < top_k receives
+// the r-th selection (id, logit). Every logit is loaded at once (lanes past E read zeros
+// without a memory access and are masked out). A round is a 32-bit wave maximum plus one ballot
+// per column to find the lowest id holding it; the value comes back from the key.
+template <int MAXC>
+MOE_DEV void topk_select(const float* __restrict__ row, int E, int top_k, int lane, int& my_i,
+                         float& my_v) {
+  const __amdgpu_buffer_rsrc_t rr = buf_rsrc(row, (uint32_t)E * 4u);
+  float v[MAXC];
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const int e = lane + 64 * c;
-    key[c] = e < E ? topk_key(row[e], e) : 0ull;
-  }
-  float my_v = 0.0f;
-  int my_i = 0;
+  for (int c = 0; c < MAXC; ++c) v[c] = __uint_as_float(buf_ld32(rr, (uint32_t)(lane + 64 * c) * 4u));
+  uint32_t key[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c)  // masked with an AND: a select of a loaded value would become
+                                  // a branch around the load with a wait inside it
+    key[c] = topk_ord(v[c]) & (0u - (uint32_t)(lane + 64 * c < E));
+  my_v = 0.0f;
+  my_i = 0;
   for (int r = 0; r < top_k; ++r) {
-    uint64_t head = 0;
+    uint32_t m = key[0];
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) head = max_u64(head, key[c]);
-    const uint64_t best = wave_max_u64(head);
-    const int e = (int)(~(uint32_t)best);
+    for (int c = 1; c < MAXC; ++c) m = max(m, key[c]);
+    m = wave_max_u32(m);
+    int sel = -1;  // lowest id whose key is the maximum (wave-uniform)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const uint64_t b = __ballot(key[c] == m);
+      if (sel < 0 && b != 0) sel = 64 * c + __ffsll((long long)b) - 1;
+    }
 #pragma unroll
     for (int c = 0; c < MAXC; ++c)
-      if (key[c] == best) key[c] = 0ull;
+      if (lane + 64 * c == sel) key[c] = 0u;
     if (lane == r) {
-      my_i = e;
-      my_v = row[e];
+      my_i = sel;
+      my_v = topk_ord_value(m);
     }
   }
+}
+
+// Renormalised weight of lane r's selection: exp(l_r - l_0) / sum_{j < k} exp(l_j - l_0).
+MOE_DEV float topk_weight(float my_v, int top_k, int lane) {
   const float vmax = __shfl(my_v, 0, 64);
   const float ex = (lane < top_k) ? expf(my_v - vmax) : 0.0f;
   float s = 0.0f;
   for (int r = 0; r < top_k; ++r) s = s + __shfl(ex, r, 64);
+  return ex / s;
+}
+
+// One wave: top-k of row[0..E) (E <= 64 * MAXC). Writes ids[t*k + r], weights[t*k + r]
+// (r < k) and, when has_shared, weights[T*k + t] = sigmoid(row[E]). Optionally mirrors the ids
+// to ids_lds.
+template <int MAXC>
+MOE_DEV void topk_token(const float* __restrict__ row, int E, int top_k, int has_shared, int T,
+                        int t, int lane, int32_t* __restrict__ ids, float* __restrict__ weights,
+                        int* ids_lds) {
+  // row[E] when has_shared, else zero; issued with the selection's loads
+  const float g = __uint_as_float(
+      buf_ld32(buf_rsrc(row, (uint32_t)(E + (has_shared ? 1 : 0)) * 4u), (uint32_t)E * 4u));
+  int my_i;
+  float my_v;
+  topk_select<MAXC>(row, E, top_k, lane, my_i, my_v);
+  const float w = topk_weight(my_v, top_k, lane);
   if (lane < top_k) {
     ids[(int64_t)t * top_k + lane] = my_i;
-    weights[(int64_t)t * top_k + lane] = ex / s;
+    weights[(int64_t)t * top_k + lane] = w;
     if (ids_lds) ids_lds[t * top_k + lane] = my_i;
   }
-  if (has_shared && lane == 0) {
-    const float g = row[E];
-    weights[(int64_t)T * top_k + t] = 1.0f / (1.0f + expf(-g));
-  }
+  if (has_shared && lane == 0) weights[(int64_t)T * top_k + t] = 1.0f / (1.0f + expf(-g));
 }
 
 // One wave: top-k of row[0..E) into LDS only (ids_lds[r], w_lds[r] for r < top_k), the same
 // selection and weights as topk_token.
+template <int MAXC>
 MOE_DEV void topk_token_lds(const float* __restrict__ row, int E, int top_k, int lane, int* ids_lds,
                             float* w_lds) {
-  constexpr int MAXC = 8;
-  uint64_t key[MAXC];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const int e = lane + 64 * c;
-    key[c] = e < E ? topk_key(row[e], e) : 0ull;
-  }
-  float my_v = 0.0f;
-  int my_i = 0;
-  for (int r = 0; r < top_k; ++r) {
-    uint64_t head = 0;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) head = max_u64(head, key[c]);
-    const uint64_t best = wave_max_u64(head);
-    const int e = (int)(~(uint32_t)best);
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c)
-      if (key[c] == best) key[c] = 0ull;
-    if (lane == r) {
-      my_i = e;
-      my_v = row[e];
-    }
-  }
-  const float vmax = __shfl(my_v, 0, 64);
-  const float ex = (lane < top_k) ? expf(my_v - vmax) : 0.0f;
-  float s = 0.0f;
-  for (int r = 0; r < top_k; ++r) s = s + __shfl(ex, r, 64);
+  int my_i;
+  float my_v;
+  topk_select<MAXC>(row, E, top_k, lane, my_i, my_v);
+  const float w = topk_weight(my_v, top_k, lane);
   if (lane < top_k) {
     ids_lds[lane] = my_i;
-    w_lds[lane] = ex / s;
+    w_lds[lane] = w;
   }
+}
+
+// topk_token / topk_token_lds for any E <= 512 (a uniform branch on E).
+MOE_DEV void topk_token_any(const float* __restrict__ row, int E, int top_k, int has_shared, int T,
+                            int t, int lane, int32_t* __restrict__ ids,
+                            float* __restrict__ weights, int* ids_lds) {
+  if (E <= 256)
+    topk_token<4>(row, E, top_k, has_shared, T, t, lane, ids, weights, ids_lds);
+  else
+    topk_token<8>(row, E, top_k, has_shared, T, t, lane, ids, weights, ids_lds);
+}
+MOE_DEV void topk_token_lds_any(const float* __restrict__ row, int E, int top_k, int lane,
+                                int* ids_lds, float* w_lds) {
+  if (E <= 256)
+    topk_token_lds<4>(row, E, top_k, lane, ids_lds, w_lds);
+  else
+    topk_token_lds<8>(row, E, top_k, lane, ids_lds, w_lds);
 }
 
 // ---------------------------------------------------------------------------- align
