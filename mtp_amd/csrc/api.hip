@@ -176,6 +176,15 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
     MOE_CHECK_HIP(launch_w2_token_sum(h, ed, sd, ids, w, out, stream), "w2 + sum");
     return MOE_OK;
   }
+  if (path == MOE_PATH_PREFILL) {  // bf16 slot rows: half the rows' HBM traffic
+    uint16_t* ys16 = at<uint16_t>(ws, L.ys);
+    MOE_CHECK_HIP(launch_w2_prefill_bf16(h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys16,
+                                         stream), "w2");
+    MOE_CHECK_HIP(launch_moe_sum_bf16(ys16, T, top_k, ex->hidden, has_shared, ids,
+                                      ex->num_experts, ex->expert_row, out, stream),
+                  "moe_sum");
+    return MOE_OK;
+  }
   if (grid)
     MOE_CHECK_HIP(launch_w2_decode_slotgrid(h, ed, sd, SlotGrid{1, nullptr, ids, w}, ys, stream),
                   "w2 (slot grid)");

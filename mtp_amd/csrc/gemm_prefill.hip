@@ -70,12 +70,13 @@ struct GroupSZ {
   uint32_t z;
 };
 
-template <int MODE>
+// YS16 (W2): the weighted slot rows are written as bf16 (round to nearest even) instead of fp32.
+template <int MODE, bool YS16 = false>
 __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
     const uint16_t* __restrict__ A,  // W1: x [T, H]; W2: h [num_slots, I]
     ExpertsDev ed, SlotsDev sd, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ eids, const int32_t* __restrict__ ntpp,
-    const float* __restrict__ topk_w, uint16_t* __restrict__ h_out, float* __restrict__ ys,
+    const float* __restrict__ topk_w, uint16_t* __restrict__ h_out, void* __restrict__ ys,
     int a_bytes, int ncolblk) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * LDS_STRIDE];
   __shared__ int s_slot[BM];
@@ -260,7 +261,12 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
           const float w = topk_w[f];
           const f32x4 o = {w * acc[mi][0][el], w * acc[mi][1][el], w * acc[mi][2][el],
                            w * acc[mi][3][el]};
-          *reinterpret_cast<f32x4*>(&ys[(int64_t)f * H + col]) = o;
+          if constexpr (YS16) {
+            const u32x2 ob = {pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3])};
+            *reinterpret_cast<u32x2*>(&static_cast<uint16_t*>(ys)[(int64_t)f * H + col]) = ob;
+          } else {
+            *reinterpret_cast<f32x4*>(&static_cast<float*>(ys)[(int64_t)f * H + col]) = o;
+          }
         }
       }
     }
@@ -282,23 +288,40 @@ hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const Slot
       a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
   const int ncb = ed.inter / 128;
-  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_W1>, dim3(xcd_grid(cap * ncb)), dim3(256), 0, stream,
-                     x, ed, sd, sorted, eids, ntpp, (const float*)nullptr, h, (float*)nullptr,
-                     (int)a_bytes, ncb);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W1>), dim3(xcd_grid(cap * ncb)), dim3(256), 0,
+                     stream, x, ed, sd, sorted, eids, ntpp, (const float*)nullptr, h,
+                     (void*)nullptr, (int)a_bytes, ncb);
   return hipGetLastError();
 }
 
-hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
-                             const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                             int BMr, int cap, const float* topk_w, float* ys,
-                             hipStream_t stream) {
+namespace {
+template <bool YS16>
+hipError_t launch_w2_prefill_t(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                               const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                               int BMr, int cap, const float* topk_w, void* ys,
+                               hipStream_t stream) {
   const int64_t a_bytes = (int64_t)sd.num_slots * ed.inter * 2;  // h [num_slots, I] bf16
   if (BMr != BM || ed.inter % BK != 0 || ed.hidden % 256 != 0 || ed.group < 64 ||
       a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
   const int ncb = ed.hidden / 256;
-  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_W2>, dim3(xcd_grid(cap * ncb)), dim3(256), 0, stream,
-                     h, ed, sd, sorted, eids, ntpp, topk_w, (uint16_t*)nullptr, ys, (int)a_bytes,
-                     ncb);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W2, YS16>), dim3(xcd_grid(cap * ncb)), dim3(256),
+                     0, stream, h, ed, sd, sorted, eids, ntpp, topk_w, (uint16_t*)nullptr, ys,
+                     (int)a_bytes, ncb);
   return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                             const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                             int BMr, int cap, const float* topk_w, float* ys,
+                             hipStream_t stream) {
+  return launch_w2_prefill_t<false>(h, ed, sd, sorted, eids, ntpp, BMr, cap, topk_w, ys, stream);
+}
+
+hipError_t launch_w2_prefill_bf16(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                                  const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                                  int BMr, int cap, const float* topk_w, uint16_t* ys,
+                                  hipStream_t stream) {
+  return launch_w2_prefill_t<true>(h, ed, sd, sorted, eids, ntpp, BMr, cap, topk_w, ys, stream);
 }

@@ -223,15 +223,26 @@ __global__ __launch_bounds__(512) void gemv_decode_kernel(const uint16_t* __rest
 }
 
 // ------------------------------------------------------------------------------- moe_sum
-// out[t] = bf16(sum over the token's slots in order of ys[slot]). With `ids`, routed slots whose
-// expert is dropped (routed_ok false: their ys rows were never written) are skipped.
+// out[t] = bf16(sum over the token's slots in order of ys[slot]) with fp32 sums; ys rows are
+// fp32 (YT = float) or bf16 (YT = uint16_t). With `ids`, routed slots whose expert is dropped
+// (routed_ok false: their ys rows were never written) are skipped.
 // Slots are taken TK at a time: all loads of a chunk are issued together as buffer loads (a
 // skipped slot or one past top_k reads zeros without a memory access, and +0 leaves the running
 // sum unchanged), so a chunk waits for three memory latencies (ids, expert_row, ys) instead of
-// one per slot. The sum runs over the slots in order.
-template <int TK>
-__global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ ys, int T,
-                                                      int top_k, int H, int has_shared,
+// one per slot.
+template <typename YT>
+MOE_DEV f32x4 ys_quad(__amdgpu_buffer_rsrc_t r, uint32_t elem_off, bool ok) {
+  if constexpr (sizeof(YT) == 4) {
+    return __builtin_bit_cast(f32x4, buf_ld128(r, ok ? elem_off * 4u : kOutOfRange));
+  } else {
+    const u32x2 v = buf_ld64(r, ok ? elem_off * 2u : kOutOfRange);
+    return f32x4{bf16lo_to_f32(v[0]), bf16hi_to_f32(v[0]), bf16lo_to_f32(v[1]), bf16hi_to_f32(v[1])};
+  }
+}
+
+template <int TK, typename YT>
+__global__ __launch_bounds__(256) void moe_sum_kernel(const YT* __restrict__ ys, int T, int top_k,
+                                                      int H, int has_shared,
                                                       const int32_t* __restrict__ ids,
                                                       int num_experts,
                                                       const int32_t* __restrict__ expert_row,
@@ -242,8 +253,8 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ 
   if (t >= T) return;
   const int c = (int)(idx % per_row) * 4;
   const int routed = T * top_k;
-  const __amdgpu_buffer_rsrc_t yr =
-      buf_rsrc(ys, (uint32_t)(routed + (has_shared ? T : 0)) * (uint32_t)H * 4u);
+  const __amdgpu_buffer_rsrc_t yr = buf_rsrc(
+      ys, (uint32_t)(routed + (has_shared ? T : 0)) * (uint32_t)H * (uint32_t)sizeof(YT));
   const __amdgpu_buffer_rsrc_t ir = buf_rsrc(ids, ids ? (uint32_t)routed * 4u : 0u);
   const __amdgpu_buffer_rsrc_t er = buf_rsrc(expert_row, expert_row ? (uint32_t)num_experts * 4u : 0u);
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -269,18 +280,36 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ 
     f32x4 v[TK];
 #pragma unroll
     for (int i = 0; i < TK; ++i)
-      v[i] = __builtin_bit_cast(
-          f32x4, buf_ld128(yr, ok[i] ? ((uint32_t)(t * top_k + i0 + i) * (uint32_t)H + (uint32_t)c) * 4u
-                                     : kOutOfRange));
+      v[i] = ys_quad<YT>(yr, (uint32_t)(t * top_k + i0 + i) * (uint32_t)H + (uint32_t)c, ok[i]);
 #pragma unroll
     for (int i = 0; i < TK; ++i) s += v[i];
   }
-  if (has_shared)
-    s += __builtin_bit_cast(f32x4, buf_ld128(yr, ((uint32_t)(routed + t) * (uint32_t)H + (uint32_t)c) * 4u));
+  if (has_shared) s += ys_quad<YT>(yr, (uint32_t)(routed + t) * (uint32_t)H + (uint32_t)c, true);
   u32x2 o;
   o[0] = pack_bf16x2(s[0], s[1]);
   o[1] = pack_bf16x2(s[2], s[3]);
   *reinterpret_cast<u32x2*>(out + (int64_t)t * H + c) = o;
+}
+
+template <typename YT>
+hipError_t launch_moe_sum_t(const YT* ys, int T, int top_k, int H, int has_shared,
+                            const int32_t* ids, int num_experts, const int32_t* expert_row,
+                            uint16_t* out, hipStream_t stream) {
+  const int64_t n = (int64_t)T * (H / 4);
+  if (n == 0) return hipSuccess;
+  if ((int64_t)(T * top_k + T) * H * (int64_t)sizeof(YT) >= kOutOfRange) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((n + 255) / 256));
+#define MOE_SUM_CASE(TKV)                                                                     \
+  if (top_k <= TKV) {                                                                         \
+    hipLaunchKernelGGL((moe_sum_kernel<TKV, YT>), grid, dim3(256), 0, stream, ys, T, top_k, H, \
+                       has_shared, ids, num_experts, expert_row, out);                        \
+    return hipGetLastError();                                                                 \
+  }
+  MOE_SUM_CASE(1) MOE_SUM_CASE(2) MOE_SUM_CASE(4) MOE_SUM_CASE(8)
+#undef MOE_SUM_CASE
+  hipLaunchKernelGGL((moe_sum_kernel<16, YT>), grid, dim3(256), 0, stream, ys, T, top_k, H,
+                     has_shared, ids, num_experts, expert_row, out);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -309,19 +338,13 @@ hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const Slots
 hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared,
                           const int32_t* ids, int num_experts, const int32_t* expert_row,
                           uint16_t* out, hipStream_t stream) {
-  const int64_t n = (int64_t)T * (H / 4);
-  if (n == 0) return hipSuccess;
-  if ((int64_t)(T * top_k + T) * H * 4 >= kOutOfRange) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((n + 255) / 256));
-#define MOE_SUM_CASE(TKV)                                                                     \
-  if (top_k <= TKV) {                                                                         \
-    hipLaunchKernelGGL(moe_sum_kernel<TKV>, grid, dim3(256), 0, stream, ys, T, top_k, H,       \
-                       has_shared, ids, num_experts, expert_row, out);                        \
-    return hipGetLastError();                                                                 \
-  }
-  MOE_SUM_CASE(1) MOE_SUM_CASE(2) MOE_SUM_CASE(4) MOE_SUM_CASE(8)
-#undef MOE_SUM_CASE
-  hipLaunchKernelGGL(moe_sum_kernel<16>, grid, dim3(256), 0, stream, ys, T, top_k, H, has_shared,
-                     ids, num_experts, expert_row, out);
-  return hipGetLastError();
+  return launch_moe_sum_t<float>(ys, T, top_k, H, has_shared, ids, num_experts, expert_row, out,
+                                 stream);
+}
+
+hipError_t launch_moe_sum_bf16(const uint16_t* ys, int T, int top_k, int H, int has_shared,
+                               const int32_t* ids, int num_experts, const int32_t* expert_row,
+                               uint16_t* out, hipStream_t stream) {
+  return launch_moe_sum_t<uint16_t>(ys, T, top_k, H, has_shared, ids, num_experts, expert_row,
+                                    out, stream);
 }

@@ -78,6 +78,10 @@ hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const Slots
 hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared,
                           const int32_t* ids, int num_experts, const int32_t* expert_row,
                           uint16_t* out, hipStream_t stream);
+// moe_sum over bf16 slot rows (summed in fp32 in slot order).
+hipError_t launch_moe_sum_bf16(const uint16_t* ys, int T, int top_k, int H, int has_shared,
+                               const int32_t* ids, int num_experts, const int32_t* expert_row,
+                               uint16_t* out, hipStream_t stream);
 
 // W2 and the weighted sum in one kernel for one or two tokens (decode path): block = token x
 // column tile, one wave per slot of the token, out written directly (no ys, no sum kernel).
@@ -95,6 +99,11 @@ hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const Slot
 hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
+// The same with bf16 slot rows (the fused layer's workspace; halves the rows' HBM traffic).
+hipError_t launch_w2_prefill_bf16(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
+                                  const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                                  int BM, int cap, const float* topk_w, uint16_t* ys,
+                                  hipStream_t stream);
 
 // Predictor MLP with L heads: z1 = h . w1^T over all L*D rows (fp32 [T][L*D+1]),
 // a = bf16(silu(z1)) head-major [L][T][D], z2[l] = a[l] . w2[l]^T (fp32 [L][T][E+1]),
