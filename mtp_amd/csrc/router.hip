@@ -105,27 +105,33 @@ __global__ __launch_bounds__(256, 2) void router_logits_rows_kernel(
   const int t0 = (wave / tiles_e) * TT;
   const int e0 = (wave % tiles_e) * TE;
   if (t0 >= T) return;
-  // Rows past the end are clamped to the last one (valid memory; their results are not stored).
-  const uint16_t* xr[TT];
-  const uint16_t* wr[TE];
+  // Buffer loads: token rows past T, router rows past the last one and steps past H read zeros
+  // without a memory access (their results are not stored), so every step issues the same
+  // loads and the waits stay exact.
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x, (uint32_t)T * (uint32_t)H * 2u);
+  const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(W, (uint32_t)E * (uint32_t)H * 2u);
+  const __amdgpu_buffer_rsrc_t srs = buf_rsrc(shared_w, shared_w ? (uint32_t)H * 2u : 0u);
+  uint32_t xo[TT], wo[TE];
 #pragma unroll
-  for (int i = 0; i < TT; ++i) xr[i] = x + (int64_t)min(t0 + i, T - 1) * H;
+  for (int i = 0; i < TT; ++i) xo[i] = t0 + i < T ? (uint32_t)(t0 + i) * (uint32_t)H * 2u : kOutOfRange;
 #pragma unroll
   for (int j = 0; j < TE; ++j) {
-    const int e = min(e0 + j, rows - 1);
-    wr[j] = e < E ? W + (int64_t)e * H : shared_w;
+    const int e = e0 + j;
+    wo[j] = e < E ? (uint32_t)e * (uint32_t)H * 2u : (e < rows ? 0u : kOutOfRange);
   }
   float acc[TT * TE];
 #pragma unroll
   for (int v = 0; v < TT * TE; ++v) acc[v] = 0.0f;
 
+  const int nsteps = H / 512;
   u32x4 xa[TT], wa[TE], xb[TT], wb[TE];
   auto load = [&](u32x4(&xv)[TT], u32x4(&wv)[TE], int step) {
-    const int off = step * 512 + lane * 8;
+    const uint32_t so = step < nsteps ? (uint32_t)(step * 512 + lane * 8) * 2u : kOutOfRange;
 #pragma unroll
-    for (int i = 0; i < TT; ++i) xv[i] = ld128(xr[i] + off);
+    for (int i = 0; i < TT; ++i) xv[i] = buf_ld128(xrs, (xo[i] + so) | (so & kOutOfRange));
 #pragma unroll
-    for (int j = 0; j < TE; ++j) wv[j] = ld128(wr[j] + off);
+    for (int j = 0; j < TE; ++j)
+      wv[j] = buf_ld128(e0 + j == E ? srs : wrs, (wo[j] + so) | (so & kOutOfRange));
   };
   auto compute = [&](const u32x4(&xv)[TT], const u32x4(&wv)[TE]) {
 #pragma unroll
@@ -141,16 +147,21 @@ __global__ __launch_bounds__(256, 2) void router_logits_rows_kernel(
       }
     }
   };
-  const int nsteps = H / 512;
+  // The next step's loads are issued before the current step's arithmetic (scheduling barriers
+  // keep them there). Steps go in pairs with both computes unconditional (a load whose only use
+  // sits under a condition would be moved into that branch, after the other step's arithmetic);
+  // an odd last step is computed after the loop, and a step past H is loaded (zeros) but never
+  // computed.
   load(xa, wa, 0);
-  for (int s = 0; s < nsteps; s += 2) {
-    if (s + 1 < nsteps) load(xb, wb, s + 1);
+  for (int s = 0; s + 1 < nsteps; s += 2) {
+    load(xb, wb, s + 1);
+    __builtin_amdgcn_sched_barrier(0);
     compute(xa, wa);
-    if (s + 1 < nsteps) {
-      if (s + 2 < nsteps) load(xa, wa, s + 2);
-      compute(xb, wb);
-    }
+    load(xa, wa, s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(xb, wb);
   }
+  if (nsteps & 1) compute(xa, wa);
 
   fold_swap32<TT * TE, 32>(acc);
   fold_swap16<TT * TE, 16>(acc);
