@@ -21,7 +21,8 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
                               int32_t* ids, float* weights, hipStream_t stream);
 // Top-k of every token (one wave each) and the align/sort of the at most 64 slots by one wave,
-// in one launch: the decode-size routing tail.
+// in one launch: the decode-size routing tail. sorted/eids are written up to the padded total
+// only (the decode kernels read nothing past it); ntpp holds the total.
 constexpr int kTopkAlignMaxTokens = 8;
 inline bool topk_align_fits(int T, int top_k, int has_shared) {
   return T >= 1 && T <= kTopkAlignMaxTokens && top_k <= 8 &&

@@ -195,12 +195,15 @@ __global__ __launch_bounds__(64 * kTopkAlignMaxTokens) void topk_align_kernel(
     int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ sorted,
     int32_t* __restrict__ eids, int32_t* __restrict__ ntpp) {
   __shared__ int s_ids[kAlignWaveMaxSlots];
+  __shared__ int s_pad[kMaxGroups];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave < T)
     topk_token_any(logits + (int64_t)wave * (E + 1), E, top_k, has_shared, T, wave, lane, ids,
                weights, s_ids);
   __syncthreads();
-  if (wave == 0) align_wave(s_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, lane);
+  if (wave == 0)
+    align_wave(s_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, lane, s_pad,
+               false);  // internal layout: the decode kernels stop at the padded total
 }
 
 template <int TT, int TE>

@@ -347,15 +347,20 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
 
 // Single-wave align for at most 64 slots (decode step sizes); same output as align_block.
 // Lane f holds slot f: the slots of one expert are found with a ballot match over the expert
-// id bits, the lowest lane of each group is its leader, and a group's offset is the sum of
-// the padded sizes of the groups with a smaller expert id (one pass over the leaders).
+// id bits and the lowest lane of each group is its leader. Each leader writes its group's padded
+// size into an LDS table indexed by group id (pad_lds, at least E + 1 ints); one exclusive scan
+// of the table by the wave gives every group's offset (groups in ascending id order), so the
+// cost does not grow with the number of distinct experts. With fill_tail false the entries past
+// the padded total (sentinels up to cap * BM, -1 block ids up to cap) are left as they are: the
+// decode kernels never read them (every block checks the padded total first).
 constexpr int kAlignWaveMaxSlots = 64;
 
 MOE_DEV void align_wave(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
                         int cap, int32_t* __restrict__ sorted, int32_t* __restrict__ eids,
-                        int32_t* __restrict__ ntpp, int lane) {
+                        int32_t* __restrict__ ntpp, int lane, int* pad_lds, bool fill_tail) {
   const int routed = T * top_k;
   const int n_slots = routed + (has_shared ? T : 0);
+  const int G = E + (has_shared ? 1 : 0);
   const int e = (lane < n_slots) ? slot_expert(topk_ids, routed, E, lane) : -1;
   const bool valid = e >= 0;
   uint64_t peers = __ballot(valid);
@@ -370,23 +375,41 @@ MOE_DEV void align_wave(const int32_t* topk_ids, int T, int top_k, int E, int ha
   const int cnt = __popcll(peers);
   const bool leader = valid && rank == 0;
   const int padded = (cnt + BM - 1) / BM * BM;
-  uint64_t leaders = __ballot(leader);
-  int off = 0, total = 0;
-  while (leaders) {
-    const int j = __ffsll((long long)leaders) - 1;
-    leaders &= leaders - 1;
-    const int ej = __shfl(e, j, 64);
-    const int pj = __shfl(padded, j, 64);
-    total += pj;
-    if (valid && ej < e) off += pj;
+
+  // padded sizes by group id, then an exclusive scan in place (lane owns a contiguous run)
+  for (int g = lane; g < G; g += 64) pad_lds[g] = 0;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave: LDS ops complete in order
+  if (leader) pad_lds[e] = padded;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int per = (G + 63) / 64;
+  const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
+  int local = 0;
+  for (int g = g0; g < g1; ++g) local += pad_lds[g];
+  int incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
   }
+  const int total = __shfl(incl, 63, 64);
+  int run = incl - local;
+  for (int g = g0; g < g1; ++g) {
+    const int pg = pad_lds[g];
+    pad_lds[g] = run;
+    run += pg;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int off = valid ? pad_lds[e] : 0;
+
   const int limit = cap * BM;
   if (valid && off + rank < limit) sorted[off + rank] = lane;
   if (leader) {
     for (int p = off + cnt; p < off + padded && p < limit; ++p) sorted[p] = n_slots;
     for (int b = off / BM; b < (off + padded) / BM && b < cap; ++b) eids[b] = e;
   }
-  for (int b = total / BM + lane; b < cap; b += 64) eids[b] = -1;
-  for (int p = total + lane; p < limit; p += 64) sorted[p] = n_slots;
+  if (fill_tail) {
+    for (int b = total / BM + lane; b < cap; b += 64) eids[b] = -1;
+    for (int p = total + lane; p < limit; p += 64) sorted[p] = n_slots;
+  }
   if (lane == 0) *ntpp = total;
 }
