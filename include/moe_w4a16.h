@@ -92,7 +92,7 @@ int moe_dequant_v1(const moe_gptq_proj_v1* proj, const int32_t* g_idx, int32_t n
  * Replaces the gate GEMV (src/mtp_expert_prefetch/mtp/extra_tensors.py:353) and vLLM
  * topk_softmax(renormalize=True) as restated at
  * src/mtp_expert_prefetch/tracing/vllm_router_trace.py:4201-4225.
- * Ties: larger logit first, equal logits -> lower expert id.
+ * Ties: larger logit first, equal logits (-0 equals +0) -> lower expert id; NaN ranks last.
  * x bf16 [T, H]; router_w bf16 [E, H]; logit_bias NULL or fp32 [E]; shared_gate_w NULL or
  * bf16 [H]. logits: fp32 workspace [T, E + 1]. topk_ids int32 [T, top_k];
  * topk_weights fp32 [T * top_k (+ T when shared_gate_w != NULL)]: entry T*top_k + t holds
