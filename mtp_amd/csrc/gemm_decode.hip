@@ -55,13 +55,22 @@ MOE_DEV bf16x8_v weight_frag(uint32_t w) {
   return as_frag(magic_pair(w, 0), magic_pair(w, 1), magic_pair(w, 2), magic_pair(w, 3));
 }
 
-// Everything one lane needs for one quantisation group (SPG MFMA k-steps of 32).
+// Everything one lane needs for one quantisation group (SPG MFMA k-steps of 32): activations
+// and packed weights, and the group's scales and zeros.
 template <int NP, int SPG, int CT>
-struct GroupBuf {
+struct GroupAW {
   u32x4 a[SPG];                 // 8 consecutive bf16 activations per k-step
   uint32_t w[NP][SPG][CT];      // packed int4 rows, CT columns
+};
+template <int NP, int CT>
+struct GroupSZ {
   uint32_t s[NP][CT / 2];       // fp16 scale pairs of the CT columns
   uint32_t z[NP];               // packed zeros word holding the CT columns
+};
+template <int NP, int SPG, int CT>
+struct GroupBuf {
+  GroupAW<NP, SPG, CT> aw;
+  GroupSZ<NP, CT> sz;
 };
 
 // A operand of one lane: resource over the activation rows and the byte offset of
@@ -101,7 +110,7 @@ struct DecodeTile {
     zgrp = (uint32_t)(NOUT / 8) * 4u;
   }
 
-  MOE_DEV void load(GroupBuf<NP, SPG, CT>& B, int gi) const {
+  MOE_DEV void load_aw(GroupAW<NP, SPG, CT>& B, int gi) const {
     const uint32_t oob = gi < ngw ? 0u : kOutOfRange;
     const uint32_t ug = (uint32_t)gi;
 #pragma unroll
@@ -121,6 +130,14 @@ struct DecodeTile {
           for (int j = 0; j < 4; ++j) B.w[p][s][j] = v[j];
         }
       }
+    }
+  }
+
+  MOE_DEV void load_sz(GroupSZ<NP, CT>& B, int gi) const {
+    const uint32_t oob = gi < ngw ? 0u : kOutOfRange;
+    const uint32_t ug = (uint32_t)gi;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
       if constexpr (CT == 2) {
         B.s[p][0] = buf_ld32(sr[p], (soff + ug * sgrp) | oob);
       } else {
@@ -132,9 +149,18 @@ struct DecodeTile {
     }
   }
 
+  MOE_DEV void load(GroupBuf<NP, SPG, CT>& B, int gi) const {
+    load_aw(B.aw, gi);
+    load_sz(B.sz, gi);
+  }
+
   // acc[p*CT + j] += s * (sum_k x (128 + q) - (128 + z) * sum_k x) over one group. A group
   // past the slice loaded zeros (scale 0) and adds +0.
   MOE_DEV void compute(const GroupBuf<NP, SPG, CT>& B, f32x4 (&acc)[NP * CT]) const {
+    compute(B.aw, B.sz, acc);
+  }
+  MOE_DEV void compute(const GroupAW<NP, SPG, CT>& B, const GroupSZ<NP, CT>& Z,
+                       f32x4 (&acc)[NP * CT]) const {
     constexpr int NT = NP * CT;
     const bf16x8_v ones = as_frag(kOnes, kOnes, kOnes, kOnes);
     f32x4 tmp[NT], tx = {0.f, 0.f, 0.f, 0.f};
@@ -157,9 +183,9 @@ struct DecodeTile {
     for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int j = 0; j < CT; ++j) {
-        const uint32_t s2 = B.s[p][j >> 1];
+        const uint32_t s2 = Z.s[p][j >> 1];
         const float sc = f16_to_f32((j & 1) ? (s2 >> 16) : (s2 & 0xFFFFu));
-        const float zb = kMagicBias + (float)((B.z[p] >> (zshift + 4 * j)) & 0xFu);
+        const float zb = kMagicBias + (float)((Z.z[p] >> (zshift + 4 * j)) & 0xFu);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           acc[p * CT + j][i] =
@@ -198,14 +224,23 @@ MOE_DEV void static_for(F&& f) {
   }
 }
 
-// decode_tile for a K slice of exactly NGW groups with every load issued up front (straight-line
-// code: group g is multiplied as soon as it has landed while the later groups are in flight).
-template <int NP, int SPG, int CT, int NGW>
-MOE_DEV void decode_tile_fixed(const DecodeTile<NP, SPG, CT>& tile, f32x4 (&acc)[NP * CT]) {
-  GroupBuf<NP, SPG, CT> ring[NGW];
-  static_for<0, NGW>([&](auto gc) { tile.load(ring[gc.value], gc.value); });
-  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
-  static_for<0, NGW>([&](auto gc) { tile.compute(ring[gc.value], acc); });
+// decode_tile for a K slice of exactly NGW groups as straight-line code: every group's scales
+// and zeros are loaded first, then a ring of DEPTH activation/weight buffers (DEPTH == NGW: all
+// loads up front). Without a loop back-edge each wait is for exactly the group about to be
+// multiplied, whatever the ring depth.
+template <int NP, int SPG, int CT, int NGW, int DEPTH>
+MOE_DEV void decode_tile_static(const DecodeTile<NP, SPG, CT>& tile, f32x4 (&acc)[NP * CT]) {
+  static_assert(DEPTH >= 1 && DEPTH <= NGW, "ring depth within the slice");
+  GroupSZ<NP, CT> sz[NGW];
+  static_for<0, NGW>([&](auto gc) { tile.load_sz(sz[gc.value], gc.value); });
+  GroupAW<NP, SPG, CT> ring[DEPTH];
+  static_for<0, DEPTH - 1>([&](auto gc) { tile.load_aw(ring[gc.value], gc.value); });
+  static_for<0, NGW>([&](auto gc) {
+    constexpr int g = gc.value;
+    if constexpr (g + DEPTH - 1 < NGW) tile.load_aw(ring[(g + DEPTH - 1) % DEPTH], g + DEPTH - 1);
+    __builtin_amdgcn_sched_barrier(0);  // this stage's loads before the wait for group g
+    tile.compute(ring[g % DEPTH], sz[g], acc);
+  });
 }
 
 MOE_DEV void projections(const ExpertsDev& ed, int mode, bool is_shared, ProjDev* pj) {
@@ -219,7 +254,10 @@ MOE_DEV void projections(const ExpertsDev& ed, int mode, bool is_shared, ProjDev
 
 // Block = one 16-slot expert block x (16 * CT) columns; KS waves split K evenly (each slice a
 // whole number of quantisation groups) and are summed through LDS in wave order.
-template <int MODE, int SPG, int KS, int CT, int NB>
+// NB > 0 and NGW == 0: runtime loop over the wave's groups with an NB-deep ring; NB < 0: a
+// slice of exactly -NB groups, all loaded up front; NGW > 0: a slice of exactly NGW groups with
+// an NB-deep ring, unrolled.
+template <int MODE, int SPG, int KS, int CT, int NB, int NGW = 0>
 __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
     const uint16_t* __restrict__ act, ExpertsDev ed, SlotsDev sd,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ eids,
@@ -311,7 +349,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   if constexpr (NB < 0) {  // fixed: the wave's slice is exactly -NB groups, all loads up front
-    decode_tile_fixed<NP, SPG, CT, -NB>(tile, acc);
+    decode_tile_static<NP, SPG, CT, -NB, -NB>(tile, acc);
+  } else if constexpr (NGW > 0) {
+    decode_tile_static<NP, SPG, CT, NGW, NB>(tile, acc);
   } else {
     decode_tile<NP, SPG, CT, NB>(tile, acc);
   }
@@ -397,7 +437,7 @@ __global__ __launch_bounds__(64 * kTokenSumMaxWaves) void w2_token_sum_kernel(
                    m == 0 ? ((uint32_t)f * (uint32_t)K + (uint32_t)(8 * kq)) * 2u : kOutOfRange};
     const DecodeTile<1, SPG, CT> tile(pj, av, NOUT, G, 0, K, cl, kq);
     if constexpr (NB < 0) {  // K is exactly -NB groups: every load up front
-      decode_tile_fixed<1, SPG, CT, -NB>(tile, acc);
+      decode_tile_static<1, SPG, CT, -NB, -NB>(tile, acc);
     } else {
       decode_tile<1, SPG, CT, NB>(tile, acc);
     }
@@ -424,7 +464,7 @@ bool decode_offsets_fit(const ExpertsDev& ed, const SlotsDev& sd) {
          (int64_t)ed.hidden * ed.inter / 2 < lim;
 }
 
-template <int MODE, int SPG, int KS, int CT, int NB>
+template <int MODE, int SPG, int KS, int CT, int NB, int NGW = 0>
 hipError_t launch_cfg(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int cap,
                       const float* topk_w, uint16_t* h, float* ys, const SlotGrid& sg,
@@ -432,8 +472,8 @@ hipError_t launch_cfg(const uint16_t* act, const ExpertsDev& ed, const SlotsDev&
   const int NOUT = (MODE == DEC_W1) ? ed.inter : ed.hidden;
   if (!decode_offsets_fit(ed, sd)) return hipErrorInvalidValue;
   const dim3 grid(NOUT / (16 * CT), sg.active ? sd.num_slots : cap);
-  hipLaunchKernelGGL((gemm_decode_kernel<MODE, SPG, KS, CT, NB>), grid, dim3(64 * KS), 0, stream,
-                     act, ed, sd, sorted, eids, ntpp, topk_w, h, ys, sg);
+  hipLaunchKernelGGL((gemm_decode_kernel<MODE, SPG, KS, CT, NB, NGW>), grid, dim3(64 * KS), 0,
+                     stream, act, ed, sd, sorted, eids, ntpp, topk_w, h, ys, sg);
   return hipGetLastError();
 }
 
@@ -450,17 +490,32 @@ hipError_t launch_group(const uint16_t* act, const ExpertsDev& ed, const SlotsDe
   }
 }
 
-// Any valid (waves per block, columns per lane, ring depth) configuration.
+// Any valid (waves per block, columns per lane, ring depth[, groups per wave]) configuration.
+// ngw > 0 selects the unrolled ring over exactly ngw groups per wave (group size 128 only).
 template <int MODE>
 hipError_t launch_decode_cfg(const uint16_t* act, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int cap, const float* topk_w, uint16_t* h, float* ys, int ks, int ct,
-                             int nb, const SlotGrid& sg, hipStream_t stream) {
+                             int nb, int ngw, const SlotGrid& sg, hipStream_t stream) {
   const int K = (MODE == DEC_W1) ? ed.hidden : ed.inter;
   const int NOUT = (MODE == DEC_W1) ? ed.inter : ed.hidden;
   if ((ct != 2 && ct != 4) || NOUT % (16 * ct) != 0 || K % (ks * ed.group) != 0)
     return hipErrorInvalidValue;
   if (nb < 0 && K / (ks * ed.group) != -nb) return hipErrorInvalidValue;
+  if (ngw > 0) {
+    if (ed.group != 128 || K / (ks * ed.group) != ngw || nb < 1 || nb > ngw)
+      return hipErrorInvalidValue;
+#define MOE_DEC_STATIC(KSV, CTV, NBV, NGWV)                                                     \
+    if (ks == KSV && ct == CTV && nb == NBV && ngw == NGWV)                                     \
+      return launch_cfg<MODE, 4, KSV, CTV, NBV, NGWV>(act, ed, sd, sorted, eids, ntpp, cap,     \
+                                                      topk_w, h, ys, sg, stream);
+    MOE_DEC_STATIC(4, 4, 2, 4) MOE_DEC_STATIC(4, 4, 3, 4) MOE_DEC_STATIC(4, 2, 2, 4)
+    MOE_DEC_STATIC(4, 2, 3, 4) MOE_DEC_STATIC(2, 2, 2, 8) MOE_DEC_STATIC(2, 2, 3, 8)
+    MOE_DEC_STATIC(2, 4, 2, 8) MOE_DEC_STATIC(2, 4, 3, 8) MOE_DEC_STATIC(1, 4, 2, 4)
+    MOE_DEC_STATIC(1, 4, 3, 4) MOE_DEC_STATIC(1, 2, 2, 4) MOE_DEC_STATIC(1, 2, 3, 4)
+#undef MOE_DEC_STATIC
+    return hipErrorInvalidValue;
+  }
 #define MOE_DEC_CASE(KSV, CTV, NBV)                                                             \
   if (ks == KSV && ct == CTV && nb == NBV)                                                      \
     return launch_group<MODE, KSV, CTV, NBV>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h,  \
@@ -479,12 +534,18 @@ hipError_t launch_decode_cfg(const uint16_t* act, const ExpertsDev& ed, const Sl
 // Configuration by problem size (measured on MI355X, 40 Zipf-skewed layers of H 2048, I 512,
 // E 256, top-8, group 128; num_slots 8 / 64 / 256 / 512 at batch 1 / 8 / 32 / 64):
 //   W1: up to 16 slots, 8 waves over K with both of a wave's groups loaded up front (7.2 us);
-//       up to 128, four waves over K with a 2-deep ring (14.4 us); up to 384, two waves (24.0 us);
-//       beyond, four waves and four columns per lane (33.1 us).
-//   W2 (K = 512, four columns per lane): two waves over K with both groups up front, except
-//       between 128 and 384 slots where one wave with a 2-deep ring is faster (12.9 vs 13.4 us).
+//       up to 384 slots, four waves over K, two columns per lane, unrolled 2-deep ring over the
+//       wave's 4 groups (13.6 us at 64 slots, 23.0 us at 256); beyond, the same with four
+//       columns per lane (31.3 us at 512).
+//   W2 (K = 512, four columns per lane): two waves over K with both groups up front (7.9 us at
+//       64 slots, 17.1 us at 512), except between 128 and 384 slots where one wave with an
+//       unrolled 2-deep ring over its 4 groups is faster (12.6 vs 13.1 us).
+// The unrolled rings exist for group size 128 and the slices above; other shapes use the
+// runtime ring with the same waves and columns.
 template <int MODE>
-void pick_decode_cfg(const ExpertsDev& ed, const SlotsDev& sd, int* ks, int* ct, int* nb) {
+void pick_decode_cfg(const ExpertsDev& ed, const SlotsDev& sd, int* ks, int* ct, int* nb,
+                     int* ngw) {
+  *ngw = 0;
   const int K = (MODE == DEC_W1) ? ed.hidden : ed.inter;
   const int groups = K / ed.group;
   const int slots = sd.num_slots;
@@ -496,22 +557,21 @@ void pick_decode_cfg(const ExpertsDev& ed, const SlotsDev& sd, int* ks, int* ct,
     }
     return false;
   };
-  auto ring = [&](int k) {  // k waves over K (fewer when K does not split), 2-deep ring
+  auto ring = [&](int k, int unrolled_groups) {  // k waves over K, 2-deep ring
     *ks = k;
     *nb = 2;
     while (*ks > 1 && K % (*ks * ed.group) != 0) *ks /= 2;
+    if (ed.group == 128 && *ks == k && K == k * 128 * unrolled_groups) *ngw = unrolled_groups;
   };
   if (MODE == DEC_W1) {
     *ct = 2;
     if (slots <= 16 && fixed(groups / 2)) return;
-    if (slots <= 128) return ring(4);
-    if (slots <= 384) return ring(2);
-    *ct = ed.inter % 64 == 0 ? 4 : 2;
-    return ring(4);
+    if (slots > 384 && ed.inter % 64 == 0) *ct = 4;
+    return ring(4, 4);
   }
   *ct = ed.hidden % 64 == 0 ? 4 : 2;
   if ((slots <= 128 || slots > 384) && fixed(groups / 2)) return;
-  ring(1);
+  ring(1, 4);
 }
 
 template <int SPG, int CT, int NB>
@@ -533,13 +593,13 @@ hipError_t launch_decode_picked(const uint16_t* act, const ExpertsDev& ed, const
                                 const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                                 int cap, const float* topk_w, uint16_t* h, float* ys,
                                 const SlotGrid& sg, hipStream_t stream) {
-  int ks, ct, nb;
-  pick_decode_cfg<MODE>(ed, sd, &ks, &ct, &nb);
+  int ks, ct, nb, ngw;
+  pick_decode_cfg<MODE>(ed, sd, &ks, &ct, &nb, &ngw);
   hipError_t e = launch_decode_cfg<MODE>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, ks,
-                                         ct, nb, sg, stream);
+                                         ct, nb, ngw, sg, stream);
   if (e == hipErrorInvalidValue)  // shape outside the tuned set: one wave, double-buffered
-    e = launch_decode_cfg<MODE>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, 1, 2, 2, sg,
-                                stream);
+    e = launch_decode_cfg<MODE>(act, ed, sd, sorted, eids, ntpp, cap, topk_w, h, ys, 1, 2, 2, 0,
+                                sg, stream);
   return e;
 }
 }  // namespace
