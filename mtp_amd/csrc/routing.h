@@ -259,7 +259,30 @@ MOE_DEV int slot_expert(const int32_t* topk_ids, int routed, int E, int f) {
   return E;  // shared slot
 }
 
-// topk_ids may point to global memory or LDS (generic address space).
+// Experts of kAlignIds consecutive chunks of a wave's slot range (slot f = base + 64 u + lane,
+// u < kAlignIds), -1 past hi or for an id outside [0, E). The id loads are buffer loads issued
+// together (slots past the routed ones read zeros without a memory access), so a batch costs one
+// memory latency instead of one per slot.
+constexpr int kAlignIds = 8;
+
+MOE_DEV void align_ids(__amdgpu_buffer_rsrc_t ir, int routed, int E, int base, int hi, int lane,
+                       int (&e)[kAlignIds]) {
+  int raw[kAlignIds];
+#pragma unroll
+  for (int u = 0; u < kAlignIds; ++u) {
+    const int f = base + 64 * u + lane;
+    raw[u] = (int)buf_ld32(ir, (f < routed && f < hi) ? (uint32_t)f * 4u : kOutOfRange);
+  }
+#pragma unroll
+  for (int u = 0; u < kAlignIds; ++u) {
+    const int f = base + 64 * u + lane;
+    const bool routed_ok = f < routed && f < hi && raw[u] >= 0 && raw[u] < E;
+    const bool shared = f >= routed && f < hi;  // the shared slots follow the routed ones
+    e[u] = routed_ok ? raw[u] : (shared ? E : -1);
+  }
+}
+
+// topk_ids in global memory.
 MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
                          int cap, int32_t* __restrict__ sorted, int32_t* __restrict__ eids,
                          int32_t* __restrict__ ntpp, AlignSmem& sm) {
@@ -272,9 +295,15 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
 
   const int per_wave = (((n_slots + kAlignWaves - 1) / kAlignWaves) + 63) / 64 * 64;
   const int lo = min(w * per_wave, n_slots), hi = min(lo + per_wave, n_slots);
-  for (int f = lo + lane; f < hi; f += 64) {
-    const int e = slot_expert(topk_ids, routed, E, f);
-    if (e >= 0) atomicAdd(&sm.cnt[w][e], 1);
+  const __amdgpu_buffer_rsrc_t ir = buf_rsrc(topk_ids, (uint32_t)routed * 4u);
+  for (int base = lo; base < hi; base += 64 * kAlignIds) {
+    int e[kAlignIds];
+    align_ids(ir, routed, E, base, hi, lane, e);
+#pragma unroll
+    for (int u = 0; u < kAlignIds; ++u) {
+      if (base + 64 * u >= hi) break;  // uniform
+      if (e[u] >= 0) atomicAdd(&sm.cnt[w][e[u]], 1);
+    }
   }
   __syncthreads();
   for (int g = tid; g < G; g += 1024) {
@@ -302,6 +331,11 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
   }
   __syncthreads();
   const int tp = sm.total_padded;
+  // Bases: one thread per group turns the 16 waves' counts into running offsets (all groups in
+  // parallel) and leaves the end of the group's real slots in pad[]. Then four threads per group
+  // write its padding sentinels with 16-byte stores (scalar stores for an unaligned head or tail)
+  // and its block ids; a group's padded end is the next group's offset.
+  const int limit = cap * BM;
   for (int g = tid; g < G; g += 1024) {
     int run = sm.off[g];
     for (int v = 0; v < kAlignWaves; ++v) {
@@ -309,11 +343,24 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
       sm.cnt[v][g] = run;
       run += c;
     }
-    const int end = sm.off[g] + sm.pad[g];
-    for (int p = run; p < end; ++p)
-      if (p < cap * BM) sorted[p] = n_slots;
-    for (int b = sm.off[g] / BM; b < end / BM; ++b)
-      if (b < cap) eids[b] = g;
+    sm.pad[g] = run;
+  }
+  __syncthreads();
+  const bool vec = (reinterpret_cast<uintptr_t>(sorted) & 15u) == 0;
+  for (int g = tid >> 2; g < G; g += 256) {
+    const int sub = tid & 3;
+    const int off = sm.off[g], real_end = sm.pad[g];
+    const int end = g + 1 < G ? sm.off[g + 1] : tp;
+    const int fend = min(end, limit);
+    const int a4 = vec ? min((real_end + 3) & ~3, fend) : fend;  // vector part [a4, v_end)
+    const int v_end = a4 + ((fend - a4) & ~3);
+    if (sub == 0) {
+      for (int p = real_end; p < a4; ++p) sorted[p] = n_slots;
+      for (int p = v_end; p < fend; ++p) sorted[p] = n_slots;
+    }
+    const i32x4 sent = {n_slots, n_slots, n_slots, n_slots};
+    for (int p = a4 + 4 * sub; p < v_end; p += 16) *reinterpret_cast<i32x4*>(&sorted[p]) = sent;
+    for (int b = off / BM + sub; b < end / BM && b < cap; b += 4) eids[b] = g;
   }
   for (int b = tp / BM + tid; b < cap; b += 1024) eids[b] = -1;
   for (int p = tp + tid; p < cap * BM; p += 1024) sorted[p] = n_slots;
@@ -322,26 +369,33 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
 
   // Stable scatter: ranges in wave order, slots in order inside a range.
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int base = lo; base < hi; base += 64) {
-    const int f = base + lane;
-    const int e = (f < hi) ? slot_expert(topk_ids, routed, E, f) : -1;
-    const bool valid = e >= 0;
-    uint64_t peers = __ballot(valid);
+  for (int base0 = lo; base0 < hi; base0 += 64 * kAlignIds) {
+    int eb[kAlignIds];
+    align_ids(ir, routed, E, base0, hi, lane, eb);
 #pragma unroll
-    for (int bit = 0; bit < 10; ++bit) {
-      const bool b = valid && ((e >> bit) & 1);
-      const uint64_t bal = __ballot(b);
-      peers &= b ? bal : ~bal;
+    for (int u = 0; u < kAlignIds; ++u) {
+      const int base = base0 + 64 * u;
+      if (base >= hi) break;  // uniform: the rest of the batch lies past the wave's range
+      const int f = base + lane;
+      const int e = eb[u];
+      const bool valid = e >= 0;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 10; ++bit) {
+        const bool b = valid && ((e >> bit) & 1);
+        const uint64_t bal = __ballot(b);
+        peers &= b ? bal : ~bal;
+      }
+      if (valid) {
+        const int rank = __popcll(peers & lt_mask);
+        const int pos = sm.cnt[w][e] + rank;
+        if (pos < cap * BM) sorted[pos] = f;
+      }
+      // wave-local LDS update after every lane has read the old base
+      __builtin_amdgcn_wave_barrier();
+      if (valid && (__ffsll((long long)peers) - 1) == lane) sm.cnt[w][e] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
     }
-    if (valid) {
-      const int rank = __popcll(peers & lt_mask);
-      const int pos = sm.cnt[w][e] + rank;
-      if (pos < cap * BM) sorted[pos] = f;
-    }
-    // wave-local LDS update after every lane has read the old base
-    __builtin_amdgcn_wave_barrier();
-    if (valid && (__ffsll((long long)peers) - 1) == lane) sm.cnt[w][e] += __popcll(peers);
-    __builtin_amdgcn_wave_barrier();
   }
 }
 
