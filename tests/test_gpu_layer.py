@@ -51,7 +51,7 @@ def test_small_layer(T, path):
 
 
 @pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode"), (16, "gemv"),
-                                    (64, "decode")])
+                                    (32, "decode"), (64, "decode")])
 def test_config1_full_shape(T, path):
     """Config 1: hidden 2048, 256 experts, intermediate 512, top-8, 16 tokens."""
     _say(f"config1 T={T} path={path}")
