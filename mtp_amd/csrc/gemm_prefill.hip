@@ -28,7 +28,6 @@ constexpr int BM = kPrefillBlockM;  // 128
 constexpr int BK = 128;             // k per step: 4 MFMA slices of 32
 constexpr int LDS_STRIDE = BK + 8;  // bf16 per LDS row (16 B padding against bank conflicts)
 constexpr int kMTiles = BM / 16;    // 8 row subtiles
-constexpr int kAChunks = BM * BK / 8 / 256;  // 16-byte A chunks per thread and step (8)
 
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
@@ -71,8 +70,10 @@ struct GroupSZ {
 };
 
 // YS16 (W2): the weighted slot rows are written as bf16 (round to nearest even) instead of fp32.
-template <int MODE, bool YS16 = false>
-__global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
+// NW waves per workgroup, each covering all BM rows x 64 GEMM columns; the block's A tile in
+// LDS is shared by the NW waves (8 waves: the tile is loaded once for twice the columns).
+template <int MODE, bool YS16 = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
     const uint16_t* __restrict__ A,  // W1: x [T, H]; W2: h [num_slots, I]
     ExpertsDev ed, SlotsDev sd, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ eids, const int32_t* __restrict__ ntpp,
@@ -94,6 +95,9 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   const int e = eids[b];
   if (!expert_ok(ed, e)) return;
 
+  constexpr int NTH = 64 * NW;                  // threads
+  constexpr int AChunks = BM * BK / 8 / NTH;    // 16-byte A chunks per thread and step
+  constexpr int ARowStep = NTH / 16;            // rows between a thread's chunks
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = ed.hidden, I = ed.inter, G = ed.group;
@@ -116,10 +120,10 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   int col;  // first of the lane's 4 projection columns
   ProjDev p;
   if (MODE == MODE_W1) {
-    col = cblk * 128 + wave * 32 + 4 * (j & 7);
+    col = cblk * (32 * NW) + wave * 32 + 4 * (j & 7);
     p = (j < 8) ? (is_shared ? ed.sgate : ed.gate) : (is_shared ? ed.sup : ed.up);
   } else {
-    col = cblk * 256 + wave * 64 + 4 * j;
+    col = cblk * (64 * NW) + wave * 64 + 4 * j;
     p = is_shared ? ed.sdown : ed.down;
   }
   const ProjDev pr = proj_row(p, is_shared ? 0 : ed.row_stride, row, K8, NG, NOUT);
@@ -128,16 +132,16 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
   const int32_t* bz = pr.qzeros + (col >> 3);
   const int zsh = 4 * (col & 7);
 
-  // ---- A staging: chunk i of this thread = row (tid >> 4) + 16 i, 16-byte k-chunk tid & 15.
+  // ---- A staging: chunk i of this thread = row (tid >> 4) + ARowStep i, 16-byte k-chunk tid & 15.
   // Buffer loads: a padding row gets an out-of-range offset, which reads zeros without a memory
   // access, while every thread still issues the same loads on every step (static wait counts).
   const int a_kc = tid & 15;
   const __amdgpu_buffer_rsrc_t a_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, a_bytes, kBufferDword3);
-  uint32_t a_off[kAChunks];  // byte offset of the chunk in A
+  uint32_t a_off[AChunks];  // byte offset of the chunk in A
 #pragma unroll
-  for (int i = 0; i < kAChunks; ++i) {
-    const int f = s_slot[(tid >> 4) + 16 * i];
+  for (int i = 0; i < AChunks; ++i) {
+    const int f = s_slot[(tid >> 4) + ARowStep * i];
     const uint32_t ar = (MODE == MODE_W1) ? slot_token(sd, f) : f;
     a_off[i] = ((unsigned)f < (unsigned)sd.num_slots) ? (ar * (uint32_t)K + a_kc * 8) * 2
                                                        : kOutOfRange;
@@ -150,20 +154,20 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(
     for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nsteps = K / BK;
-  u32x4 ra[kAChunks / 2];  // one half of a step's A chunks in flight
+  u32x4 ra[AChunks / 2];   // one half of a step's A chunks in flight
   u32x4 bw[4];             // packed weight words of the 4 k-slices of a step
   GroupSZ gz[2];           // groups of k-slices 0-1 and 2-3 (the same group when G >= 128)
   auto load_a = [&](int step, int half) {
 #pragma unroll
-    for (int i = 0; i < kAChunks / 2; ++i)
+    for (int i = 0; i < AChunks / 2; ++i)
       ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            a_rsrc, a_off[half * (kAChunks / 2) + i] + step * BK * 2,
+                                            a_rsrc, a_off[half * (AChunks / 2) + i] + step * BK * 2,
                                             0, 0));
   };
   auto store_a = [&](uint16_t* la, int half) {
 #pragma unroll
-    for (int i = 0; i < kAChunks / 2; ++i) {
-      const int r = (tid >> 4) + 16 * (half * (kAChunks / 2) + i);
+    for (int i = 0; i < AChunks / 2; ++i) {
+      const int r = (tid >> 4) + ARowStep * (half * (AChunks / 2) + i);
       *reinterpret_cast<u32x4*>(&la[r * LDS_STRIDE + a_kc * 8]) = ra[i];
     }
   };
@@ -280,6 +284,8 @@ int xcd_grid(int items) { return ((items + 7) / 8) * 8; }
 
 // Shapes (checked by the entry points): hidden % 512 == 0, intermediate in {256, 512, 1024},
 // group in {64, 128, 256}; so K % 128 == 0, W1 columns % 128 == 0 and W2 columns % 256 == 0.
+// Four waves per workgroup (two workgroups per CU): measured faster than eight waves sharing one
+// A tile over twice the columns (W1 160 vs 179 us at T = 2048), which leaves one workgroup per CU.
 hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              int BMr, int cap, uint16_t* h, hipStream_t stream) {
@@ -288,8 +294,8 @@ hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const Slot
       a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
   const int ncb = ed.inter / 128;
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W1>), dim3(xcd_grid(cap * ncb)), dim3(256), 0,
-                     stream, x, ed, sd, sorted, eids, ntpp, (const float*)nullptr, h,
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W1, false, 4>), dim3(xcd_grid(cap * ncb)),
+                     dim3(256), 0, stream, x, ed, sd, sorted, eids, ntpp, (const float*)nullptr, h,
                      (void*)nullptr, (int)a_bytes, ncb);
   return hipGetLastError();
 }
@@ -305,9 +311,9 @@ hipError_t launch_w2_prefill_t(const uint16_t* h, const ExpertsDev& ed, const Sl
       a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
   const int ncb = ed.hidden / 256;
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W2, YS16>), dim3(xcd_grid(cap * ncb)), dim3(256),
-                     0, stream, h, ed, sd, sorted, eids, ntpp, topk_w, (uint16_t*)nullptr, ys,
-                     (int)a_bytes, ncb);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W2, YS16, 4>), dim3(xcd_grid(cap * ncb)),
+                     dim3(256), 0, stream, h, ed, sd, sorted, eids, ntpp, topk_w,
+                     (uint16_t*)nullptr, ys, (int)a_bytes, ncb);
   return hipGetLastError();
 }
 }  // namespace
