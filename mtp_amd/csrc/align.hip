@@ -22,6 +22,167 @@ __global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__
   align_block(topk_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, sm);
 }
 
+// ---- Two-kernel align for large inputs (prefill): chunk ranks in parallel, then one block.
+// Kernel 1: workgroup c (one wave) ranks the slots of chunk c = [c CH, (c + 1) CH) by expert in
+// slot order (the ballot match of align_block, 64 slots at a time) and writes, into the sorted
+// buffer used as scratch, each slot's rank inside its chunk at sorted[f] and the chunk's
+// per-group counts at sorted[n_slots + c G + g].
+// Kernel 2 (one 1024-thread block): reads all counts into LDS and its slots' ranks into
+// registers, and only after a barrier writes the final layout: per-group bases per chunk, group
+// offsets (exclusive scan of padded sizes), padding sentinels and block ids, then every slot at
+// offset + chunk base + rank. The result is the single-block layout: experts ascending, slots
+// ascending inside an expert.
+constexpr int kAlign2MaxChunks = 64;
+constexpr int kAlign2LdsCounts = 16448;       // chunks x groups held in LDS by kernel 2
+constexpr int kAlign2MaxSlotsPerThread = 32;  // kernel 2's registers: slots of one thread
+
+__global__ __launch_bounds__(64) void align_chunk_kernel(const int32_t* __restrict__ topk_ids,
+                                                         int T, int top_k, int E, int has_shared,
+                                                         int CH, int32_t* __restrict__ scratch) {
+  __shared__ int cnt[kMaxGroups];
+  const int lane = threadIdx.x, c = blockIdx.x;
+  const int routed = T * top_k;
+  const int n_slots = routed + (has_shared ? T : 0);
+  const int G = E + (has_shared ? 1 : 0);
+  for (int g = lane; g < G; g += 64) cnt[g] = 0;
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave: LDS ops complete in order
+  const int lo = min(c * CH, n_slots), hi = min(lo + CH, n_slots);
+  const __amdgpu_buffer_rsrc_t ir = buf_rsrc(topk_ids, (uint32_t)routed * 4u);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base0 = lo; base0 < hi; base0 += 64 * kAlignIds) {
+    int eb[kAlignIds];
+    align_ids(ir, routed, E, base0, hi, lane, eb);
+#pragma unroll
+    for (int u = 0; u < kAlignIds; ++u) {
+      const int f = base0 + 64 * u + lane;
+      if (base0 + 64 * u >= hi) break;  // uniform
+      const int e = eb[u];
+      const bool valid = e >= 0;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 10; ++bit) {
+        const bool b = valid && ((e >> bit) & 1);
+        const uint64_t bal = __ballot(b);
+        peers &= b ? bal : ~bal;
+      }
+      if (valid) scratch[f] = cnt[e] + __popcll(peers & lt_mask);
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (valid && (__ffsll((long long)peers) - 1) == lane) cnt[e] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
+  for (int g = lane; g < G; g += 64) scratch[n_slots + c * G + g] = cnt[g];
+}
+
+__global__ __launch_bounds__(1024) void align_finish_kernel(
+    const int32_t* __restrict__ topk_ids, int T, int top_k, int E, int has_shared, int BM,
+    int cap, int CH, int nchunks, int32_t* __restrict__ sorted, int32_t* __restrict__ eids,
+    int32_t* __restrict__ ntpp) {
+  __shared__ int cl[kAlign2LdsCounts];  // [chunk][group]: counts, then bases inside the group
+  __shared__ int s_off[kMaxGroups], s_pad[kMaxGroups];
+  __shared__ int s_total;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int routed = T * top_k;
+  const int n_slots = routed + (has_shared ? T : 0);
+  const int G = E + (has_shared ? 1 : 0);
+  // 1. everything this block reads from the scratch, before anything is written
+  {  // 16 count loads per thread in flight together (buffer loads; past the end: zeros)
+    constexpr int NL = (kAlign2LdsCounts + 1023) / 1024;
+    const int ncnt = nchunks * G;
+    const __amdgpu_buffer_rsrc_t cr = buf_rsrc(sorted + n_slots, (uint32_t)ncnt * 4u);
+    int v[NL];
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int i = tid + 1024 * k;
+      v[k] = (int)buf_ld32(cr, i < ncnt ? (uint32_t)i * 4u : kOutOfRange);
+    }
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int i = tid + 1024 * k;
+      if (i < kAlign2LdsCounts) cl[i] = v[k];
+    }
+  }
+  // ranks and raw ids of this thread's slots, all in flight together; the ids are decoded only
+  // in the scatter below (a select on a loaded value here would become a branch with a wait)
+  int rk[kAlign2MaxSlotsPerThread], raw[kAlign2MaxSlotsPerThread];
+  const __amdgpu_buffer_rsrc_t ir = buf_rsrc(topk_ids, (uint32_t)routed * 4u);
+  const __amdgpu_buffer_rsrc_t sr = buf_rsrc(sorted, (uint32_t)n_slots * 4u);
+#pragma unroll
+  for (int i = 0; i < kAlign2MaxSlotsPerThread; ++i) {
+    const int f = tid + 1024 * i;
+    rk[i] = (int)buf_ld32(sr, f < n_slots ? (uint32_t)f * 4u : kOutOfRange);
+    raw[i] = (int)buf_ld32(ir, f < routed ? (uint32_t)f * 4u : kOutOfRange);
+  }
+  // every scratch read has returned before any thread of the block overwrites the buffer
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // 2. per group: bases of the chunks (running counts) and the padded size
+  for (int g = tid; g < G; g += 1024) {
+    int run = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      const int n = cl[c * G + g];
+      cl[c * G + g] = run;
+      run += n;
+    }
+    s_pad[g] = run;  // the group's slot count for now
+  }
+  __syncthreads();
+  // 3. group offsets: exclusive scan of the padded sizes by one wave
+  if (w == 0) {
+    const int per = (G + 63) / 64;
+    const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
+    int local = 0;
+    for (int g = g0; g < g1; ++g) local += (s_pad[g] + BM - 1) / BM * BM;
+    int incl = local;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    int run = incl - local;
+    for (int g = g0; g < g1; ++g) {
+      s_off[g] = run;
+      run += (s_pad[g] + BM - 1) / BM * BM;
+    }
+    if (lane == 63) s_total = incl;
+  }
+  __syncthreads();
+  const int tp = s_total;
+  const int limit = cap * BM;
+  // 4. padding sentinels (four threads per group, 16-byte stores) and block ids
+  const bool vec = (reinterpret_cast<uintptr_t>(sorted) & 15u) == 0;
+  for (int g = tid >> 2; g < G; g += 256) {
+    const int sub = tid & 3;
+    const int off = s_off[g], real_end = off + s_pad[g];
+    const int end = g + 1 < G ? s_off[g + 1] : tp;
+    const int fend = min(end, limit);
+    const int a4 = vec ? min((real_end + 3) & ~3, fend) : fend;
+    const int v_end = a4 + ((fend - a4) & ~3);
+    if (sub == 0) {
+      for (int p = real_end; p < a4; ++p) sorted[p] = n_slots;
+      for (int p = v_end; p < fend; ++p) sorted[p] = n_slots;
+    }
+    const i32x4 sent = {n_slots, n_slots, n_slots, n_slots};
+    for (int p = a4 + 4 * sub; p < v_end; p += 16) *reinterpret_cast<i32x4*>(&sorted[p]) = sent;
+    for (int b = off / BM + sub; b < end / BM && b < cap; b += 4) eids[b] = g;
+  }
+  for (int b = tp / BM + tid; b < cap; b += 1024) eids[b] = -1;
+  for (int p = tp + tid; p < limit; p += 1024) sorted[p] = n_slots;
+  if (tid == 0) *ntpp = tp;
+  // 5. the slots
+#pragma unroll
+  for (int i = 0; i < kAlign2MaxSlotsPerThread; ++i) {
+    const int f = tid + 1024 * i;
+    const int e = f < routed ? ((raw[i] >= 0 && raw[i] < E) ? raw[i] : -1) : (f < n_slots ? E : -1);
+    if (e >= 0) {
+      const int pos = s_off[e] + cl[(f / CH) * G + e] + rk[i];
+      if (pos < limit) sorted[pos] = f;
+    }
+  }
+}
+
 }  // namespace
 
 int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM) {
@@ -34,6 +195,24 @@ int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM) {
 hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
                         int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp,
                         hipStream_t stream) {
+  const int n_slots = T * top_k + (has_shared ? T : 0);
+  const int G = E + (has_shared ? 1 : 0);
+  // Large inputs with room for the scratch in the sorted buffer: two kernels.
+  int nchunks = kAlign2LdsCounts / G;
+  if (nchunks > kAlign2MaxChunks) nchunks = kAlign2MaxChunks;
+  const int CH = nchunks > 0 ? ((n_slots + nchunks - 1) / nchunks + 63) / 64 * 64 : 0;
+  if (n_slots >= 4096 && BM >= 64 && nchunks > 0 &&
+      n_slots <= 1024 * kAlign2MaxSlotsPerThread && G <= kMaxGroups &&
+      (int64_t)cap * BM >= (int64_t)n_slots + (int64_t)nchunks * G) {
+    nchunks = (n_slots + CH - 1) / CH;
+    hipLaunchKernelGGL(align_chunk_kernel, dim3(nchunks), dim3(64), 0, stream, topk_ids, T,
+                       top_k, E, has_shared, CH, sorted);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(align_finish_kernel, dim3(1), dim3(1024), 0, stream, topk_ids, T, top_k, E,
+                       has_shared, BM, cap, CH, nchunks, sorted, eids, ntpp);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, topk_ids, T, top_k, E,
                      has_shared, BM, cap, sorted, eids, ntpp);
   return hipGetLastError();
