@@ -3,11 +3,13 @@
 // used at src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19647-19660; the format's
 // known-answer test is tests/test_vllm_descriptor_mapping_assertion.py:1012-1085).
 //
-// One workgroup of 16 waves (routing.h:align_block). Wave w owns a contiguous range of slots.
-// Pass 1 builds per-wave expert histograms in LDS; pass 2 turns them into exclusive
-// per-(wave, expert) base positions; pass 3 walks each range 64 slots at a time in slot order,
-// ranks equal experts inside the wave with a ballot-based match, and scatters. The order is
-// therefore experts ascending, slots ascending within an expert - a stable argsort.
+// Decode sizes: one workgroup of 16 waves (routing.h:align_block). Wave w owns a contiguous
+// range of slots. Pass 1 builds per-wave expert histograms in LDS; pass 2 turns them into
+// exclusive per-(wave, expert) base positions; pass 3 walks each range 64 slots at a time in slot
+// order, ranks equal experts inside the wave with a ballot-based match, and scatters. The order
+// is therefore experts ascending, slots ascending within an expert - a stable argsort.
+// Large inputs (prefill): the same ranking per chunk in many single-wave workgroups, then one
+// block for the offsets and the scatter (align_chunk_kernel / align_finish_kernel below).
 #include "launch.h"
 #include "routing.h"
 
