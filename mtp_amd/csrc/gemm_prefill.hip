@@ -12,13 +12,19 @@
 //   B operand straight from the GPTQ layout: for each 32-k slice, lane (j = lane & 15,
 //   kq = lane >> 4) loads 16 bytes = the packed words of 4 consecutive columns c_j .. c_j + 3
 //   at packed row kq; word ni is exactly the MFMA B fragment (8 consecutive k of one column)
-//   of column tile ni, so tile ni holds the columns {c_j + ni}.
-//   A operand (gathered bf16 rows) is staged in LDS, 128 k per step, double-buffered so one
-//   barrier per step orders both the writes and the reuse of a buffer.
+//   of column tile ni, so tile ni holds the columns {c_j + ni}. A two-step register ring keeps
+//   the next two 128-k steps of B in flight.
+//   A operand (gathered bf16 rows) is loaded straight into LDS (buffer_load ... lds, no VGPR
+//   staging), 128 k per step, double-buffered: the next step's tile is in flight during a step,
+//   and one wait + barrier per step orders both its arrival and the reuse of a buffer.
 //   W1: a wave's 64 columns are 32 gate columns (lanes j < 8) and the same 32 up columns
 //       (lanes j >= 8); the epilogue pairs them with a row rotation by 8 and writes bf16 h.
-//   W2: 64 output columns of the hidden dimension; epilogue writes w[slot] * acc (fp32).
-// 16-row subtiles that hold only padding are neither loaded nor multiplied.
+//   W2: 64 output columns of the hidden dimension; epilogue writes w[slot] * acc (fp32 or bf16).
+// 16-row subtiles that hold only padding are neither loaded nor multiplied. Blocks with at most
+// two subtiles of slots (experts with few tokens) take a streaming path instead: no LDS, a
+// register ring several k-steps deep (see stream_block).
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -26,8 +32,29 @@ namespace {
 
 constexpr int BM = kPrefillBlockM;  // 128
 constexpr int BK = 128;             // k per step: 4 MFMA slices of 32
-constexpr int LDS_STRIDE = BK + 8;  // bf16 per LDS row (16 B padding against bank conflicts)
 constexpr int kMTiles = BM / 16;    // 8 row subtiles
+// Loads per step of the LDS path's B ring (scales + zeros of two half-steps, 4 weight words),
+// the count the wait for a step's A tile leaves in flight.
+constexpr int kLoadsPerStepB = 8;
+
+// s_waitcnt immediate waiting for vmcnt <= n only (expcnt and lgkmcnt at their maximum).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Buffer load of 16 bytes per lane straight into LDS: lane i writes lds[16 i, 16 i + 16) (bytes;
+// lds wave-uniform). An out-of-range offset writes zeros. (A device function: the builtin
+// inside a lambda of a kernel makes the host pass drop the kernel's launch stub.)
+MOE_DEV void buf_ld128_lds(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, off, 0, 0, 0);
+}
+
+// Streaming path: blocks of at most kStreamMaxTiles row subtiles; ring depth (k-steps in
+// flight per wave) for one and for two subtiles. K is a multiple of 256, so the step count is
+// even (the runtime-count ring is 2 deep).
+constexpr int kStreamMaxTiles = 2;
+constexpr int kStreamDepth1 = 4;
+constexpr int kStreamDepth2 = 3;
 
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
@@ -69,6 +96,167 @@ struct GroupSZ {
   uint32_t z;
 };
 
+// fp16 scales and c = -(1024 + z) * s of the lane's 4 columns (zero nibbles from bit zsh).
+MOE_DEV void group_coeffs(const GroupSZ& q, int zsh, _Float16 (&sc)[4], float (&cc)[4]) {
+  const uint32_t zw = q.z >> zsh;
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    sc[n] = __builtin_bit_cast(_Float16, (uint16_t)(q.s[n >> 1] >> (16 * (n & 1))));
+    cc[n] = -(1024.0f + (float)((zw >> (4 * n)) & 0xFu)) * (float)sc[n];
+  }
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+MOE_DEV void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// ---- Streaming path for blocks whose slots fit in MT row subtiles (an expert with few tokens).
+// Such a block reads its 128 KB-per-wave weight slice for very little arithmetic, so its time is
+// memory latency: with the LDS-staged path's one-step lookahead every 128-k step waits for a
+// full round trip. Here each wave keeps D k-steps in flight in registers - the A fragments of
+// its MT row subtiles, the packed weight words and the step's scales and zeros, all buffer loads
+// (steps past K read zeros without a memory access) - and uses no LDS and no barrier. The
+// arithmetic (exact dequant, MFMA order over k) is the LDS path's.
+template <int MT>
+struct StreamStage {
+  u32x4 a[MT][4];  // row mi*16 + j, 8 consecutive bf16 at k = 32 kk + 8 kq
+  u32x4 bw[4];     // packed words of the lane's 4 columns, k-slice kk
+  GroupSZ gz[2];   // groups of k-slices 0-1 and 2-3
+};
+
+struct StreamView {
+  __amdgpu_buffer_rsrc_t ar;  // A rows (uniform)
+  uint32_t a_off[2];          // lane row offsets (+ 8 kq bf16), kOutOfRange for a padding row
+  // The lane's weights: in W1 lanes j < 8 read gate and lanes j >= 8 up, so these are per-lane
+  // global addresses rather than buffer resources.
+  const int32_t* bq;          // packed row kq of step 0 at the lane's first column
+  const uint16_t* bs;         // scales of group 0 at the lane's first column
+  const int32_t* bz;          // zeros word of group 0 holding the lane's columns
+  int NOUT, G, nsteps, zsh;
+
+  // Step s of the ring; a prefetch past the last step re-reads the last step (in bounds; it is
+  // never multiplied), so every pass issues the same loads.
+  template <int MT>
+  MOE_DEV void load(StreamStage<MT>& st, int s) const {
+    const int sc = min(s, nsteps - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int g = (sc * BK + 64 * h) / G;
+      st.gz[h].s = *reinterpret_cast<const u32x2*>(bs + (int64_t)g * NOUT);
+      st.gz[h].z = (uint32_t)bz[(int64_t)g * (NOUT / 8)];
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)  // weights are streamed once: nontemporal
+      st.bw[kk] = ld128_nt(bq + (int64_t)(sc * (BK / 8) + kk * 4) * NOUT);
+    const uint32_t ka = (uint32_t)sc * BK * 2u;
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) st.a[mi][kk] = buf_ld128(ar, a_off[mi] + ka + 64u * kk);
+  }
+
+  template <int MT>
+  MOE_DEV void compute(const StreamStage<MT>& st, f32x4 (&acc)[MT][4]) const {
+    _Float16 sc[4];
+    float cc[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if ((kk & 1) == 0) group_coeffs(st.gz[kk >> 1], zsh, sc, cc);
+      bf16x8_v bfr[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) bfr[n] = dequant8_exact(st.bw[kk][n], sc[n], cc[n]);
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi) {
+        const bf16x8_v af = __builtin_bit_cast(bf16x8_v, st.a[mi][kk]);
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          acc[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[n], acc[mi][n], 0, 0, 0);
+      }
+    }
+  }
+};
+
+// acc += A[MT*16 rows, :K] . B[:K, lane columns] over all steps with a D-deep register ring.
+// NS > 0: exactly NS steps as straight-line code, so each wait is for exactly the step about to be
+// multiplied. NS == 0: a runtime loop (D divides the step count) whose body issues the same loads
+// on every pass; its waits are exact only for D == 2 (a deeper ring makes the loop head wait for
+// all but the newest stage).
+template <int MT, int D, int NS>
+MOE_DEV void stream_block(const StreamView& v, f32x4 (&acc)[MT][4]) {
+  StreamStage<MT> ring[D];
+  static_for<0, D - 1>([&](auto jc) {
+    v.load(ring[jc.value], jc.value);
+    __builtin_amdgcn_sched_barrier(0);  // issue order = step order
+  });
+  if constexpr (NS > 0) {
+    static_for<0, NS>([&](auto sc) {
+      constexpr int st = sc.value;
+      if constexpr (st + D - 1 < NS) v.load(ring[(st + D - 1) % D], st + D - 1);
+      __builtin_amdgcn_sched_barrier(0);  // this stage's loads ahead of the wait for step st
+      v.compute(ring[st % D], acc);
+    });
+  } else {
+    for (int s0 = 0; s0 < v.nsteps; s0 += D) {
+      static_for<0, D>([&](auto jc) {
+        constexpr int jj = jc.value;
+        v.load(ring[(jj + D - 1) % D], s0 + jj + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        v.compute(ring[jj], acc);
+      });
+    }
+  }
+}
+
+// Epilogue of the first `mtiles` row subtiles. D[i][jj] of a 16x16 tile sits in lane
+// jj + 16*(i/4), element i%4; column jj of tile n is projection column col(jj) + n.
+template <int MODE, bool YS16, int M>
+MOE_DEV void block_epilogue(const f32x4 (&acc)[M][4], int mtiles, const int* s_slot, int j,
+                            int kq, int col, int num_slots, int I, int H,
+                            const float* s_w, uint16_t* __restrict__ h_out,
+                            void* __restrict__ ys) {
+#pragma unroll
+  for (int mi = 0; mi < M; ++mi) {
+    if (mi >= mtiles) break;
+#pragma unroll
+    for (int el = 0; el < 4; ++el) {
+      const int r = mi * 16 + 4 * kq + el;
+      const int f = s_slot[r];
+      if (MODE == MODE_W1) {
+        float hv[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const float g = acc[mi][n][el];
+          // lanes jj < 8 hold gate, lane jj + 8 the up value of the same column (row_ror:8)
+          const float u = __int_as_float(
+              __builtin_amdgcn_update_dpp(0, __float_as_int(g), 0x128, 0xF, 0xF, false));
+          hv[n] = silu_f32(g) * u;
+        }
+        if (j < 8 && (unsigned)f < (unsigned)num_slots) {
+          const u32x2 o = {pk_bf16(hv[0], hv[1]), pk_bf16(hv[2], hv[3])};
+          *reinterpret_cast<u32x2*>(&h_out[(int64_t)f * I + col]) = o;
+        }
+      } else {
+        if ((unsigned)f < (unsigned)num_slots) {
+          const float w = s_w[r];
+          const f32x4 o = {w * acc[mi][0][el], w * acc[mi][1][el], w * acc[mi][2][el],
+                           w * acc[mi][3][el]};
+          if constexpr (YS16) {
+            const u32x2 ob = {pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3])};
+            *reinterpret_cast<u32x2*>(&static_cast<uint16_t*>(ys)[(int64_t)f * H + col]) = ob;
+          } else {
+            *reinterpret_cast<f32x4*>(&static_cast<float*>(ys)[(int64_t)f * H + col]) = o;
+          }
+        }
+      }
+    }
+  }
+}
+
 // YS16 (W2): the weighted slot rows are written as bf16 (round to nearest even) instead of fp32.
 // NW waves per workgroup, each covering all BM rows x 64 GEMM columns; the block's A tile in
 // LDS is shared by the NW waves (8 waves: the tile is loaded once for twice the columns).
@@ -79,13 +267,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
     const int32_t* __restrict__ eids, const int32_t* __restrict__ ntpp,
     const float* __restrict__ topk_w, uint16_t* __restrict__ h_out, void* __restrict__ ys,
     int a_bytes, int ncolblk) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * LDS_STRIDE];
+  // Two A buffers as separate objects: the compiler then knows that reads of one do not wait
+  // for the LDS loads in flight into the other.
+  __shared__ __attribute__((aligned(16))) uint16_t lds_a0[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_a1[BM * BK];
   __shared__ int s_slot[BM];
+  __shared__ float s_w[MODE == MODE_W2 ? BM : 1];  // routed weight of each row (W2)
 
   // XCD-aware order: workgroup p runs on XCD p % 8, and XCD c takes the contiguous range
   // [c S, c S + S) of the used (align block, column block) items, numbered expert-major, so the
-  // column blocks of one align block (same A rows) and the align blocks of one expert (same
-  // weights) run close together on one XCD and share its L2.
+  // column blocks of one align block (same A rows) run back to back on one XCD and share the
+  // rows in its L2. (Dealing whole blocks to the XCDs in turn evens out their work - a few hot
+  // experts' full blocks otherwise land on some XCDs - but measured no faster.)
   const int used = (*ntpp / BM) * ncolblk;
   const int per_xcd = (used + 7) / 8;
   const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
@@ -95,9 +288,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   const int e = eids[b];
   if (!expert_ok(ed, e)) return;
 
-  constexpr int NTH = 64 * NW;                  // threads
-  constexpr int AChunks = BM * BK / 8 / NTH;    // 16-byte A chunks per thread and step
-  constexpr int ARowStep = NTH / 16;            // rows between a thread's chunks
+  constexpr int kARowsPerWave = BM / NW;       // A rows each wave loads into LDS per step
+  constexpr int kADmaLoads = kARowsPerWave / 4;  // 1 KB (4-row) LDS loads per wave and step
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = ed.hidden, I = ed.inter, G = ed.group;
@@ -107,7 +299,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   const int64_t row = is_shared ? 0 : expert_row(ed, e);
   const int K8 = K / 8, NG = K / G;
 
-  if (tid < BM) s_slot[tid] = sorted[b * BM + tid];
+  if (tid < BM) {
+    const int f = sorted[b * BM + tid];
+    s_slot[tid] = f;
+    if constexpr (MODE == MODE_W2) s_w[tid] = (unsigned)f < (unsigned)sd.num_slots ? topk_w[f] : 0.0f;
+  }
   __syncthreads();
   // Valid rows come first in a block (an expert's slots, then its padding).
   int nvalid = 0;
@@ -132,20 +328,82 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   const int32_t* bz = pr.qzeros + (col >> 3);
   const int zsh = 4 * (col & 7);
 
-  // ---- A staging: chunk i of this thread = row (tid >> 4) + ARowStep i, 16-byte k-chunk tid & 15.
-  // Buffer loads: a padding row gets an out-of-range offset, which reads zeros without a memory
-  // access, while every thread still issues the same loads on every step (static wait counts).
-  const int a_kc = tid & 15;
-  const __amdgpu_buffer_rsrc_t a_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, a_bytes, kBufferDword3);
-  uint32_t a_off[AChunks];  // byte offset of the chunk in A
+  // Few slots: the streaming path (no LDS, a register ring several k-steps deep).
+  const int mt_u = __builtin_amdgcn_readfirstlane(mtiles);
+  if (mt_u <= kStreamMaxTiles) {
+    const __amdgpu_buffer_rsrc_t ar =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, a_bytes, kBufferDword3);
+    StreamView v;
+    v.ar = ar;
 #pragma unroll
-  for (int i = 0; i < AChunks; ++i) {
-    const int f = s_slot[(tid >> 4) + ARowStep * i];
+    for (int mi = 0; mi < 2; ++mi) {
+      const int f = s_slot[mi * 16 + j];
+      const uint32_t arow = (MODE == MODE_W1) ? slot_token(sd, f) : f;
+      v.a_off[mi] = ((unsigned)f < (unsigned)sd.num_slots)
+                        ? (arow * (uint32_t)K + 8u * kq) * 2u
+                        : kOutOfRange;
+    }
+    v.bq = bq;
+    v.bs = bs;
+    v.bz = bz;
+    v.NOUT = NOUT;
+    v.G = G;
+    v.nsteps = K / BK;
+    v.zsh = zsh;
+    // step count of the usual shapes (hidden 2048, intermediate 512): a straight-line ring
+    constexpr int kNS = (MODE == MODE_W1) ? 16 : 4;
+    if (mt_u == 1) {
+      f32x4 acc1[1][4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) acc1[0][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (v.nsteps == kNS) {
+        stream_block<1, kStreamDepth1, kNS>(v, acc1);
+      } else {
+        stream_block<1, 2, 0>(v, acc1);
+      }
+      block_epilogue<MODE, YS16>(acc1, 1, s_slot, j, kq, col, sd.num_slots, I, H, s_w, h_out,
+                                 ys);
+    } else {
+      f32x4 acc2[2][4];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc2[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (v.nsteps == kNS) {
+        stream_block<2, kStreamDepth2, kNS>(v, acc2);
+      } else {
+        stream_block<2, 2, 0>(v, acc2);
+      }
+      block_epilogue<MODE, YS16>(acc2, 2, s_slot, j, kq, col, sd.num_slots, I, H, s_w, h_out,
+                                 ys);
+    }
+    return;
+  }
+
+  // ---- A tile in LDS: BM rows x BK k per step, rows of BK bf16 (256 B) without padding; the
+  // 16-byte chunk c of row r sits at chunk position c ^ (r & 15), so the 16 rows one MFMA A read
+  // spans fall in 16 different bank groups. The tile is loaded straight into LDS
+  // (buffer_load ... lds): lane i of one load writes bytes [16 i, 16 i + 16) of a 1 KB run of 4
+  // rows, so it fetches row 4q + (i >> 4) of the run at k-chunk (i & 15) ^ row. Wave w fills rows
+  // [w BM/NW, (w + 1) BM/NW); a padding row gets an out-of-range offset (zeros, no memory access).
+  const __amdgpu_buffer_rsrc_t a_rsrc = buf_rsrc(A, (uint32_t)a_bytes);
+  uint32_t a_off[kADmaLoads];  // byte offset of this lane's chunk of load i, step 0
+#pragma unroll
+  for (int i = 0; i < kADmaLoads; ++i) {
+    const int r = wave * kARowsPerWave + 4 * i + (lane >> 4);
+    const int f = s_slot[r];
     const uint32_t ar = (MODE == MODE_W1) ? slot_token(sd, f) : f;
-    a_off[i] = ((unsigned)f < (unsigned)sd.num_slots) ? (ar * (uint32_t)K + a_kc * 8) * 2
+    const uint32_t c = (uint32_t)((lane & 15) ^ (r & 15));
+    a_off[i] = ((unsigned)f < (unsigned)sd.num_slots) ? (ar * (uint32_t)K + 8u * c) * 2u
                                                        : kOutOfRange;
   }
+  const int nsteps = K / BK;
+  auto dma_a = [&](uint16_t* buf, int step) {  // a step past K writes zeros (never read)
+    const uint32_t ko = (uint32_t)step * BK * 2u | (step < nsteps ? 0u : kOutOfRange);
+#pragma unroll
+    for (int i = 0; i < kADmaLoads; ++i)
+      buf_ld128_lds(a_rsrc, buf + (wave * kARowsPerWave + 4 * i) * BK, a_off[i] + ko);
+  };
 
   f32x4 acc[kMTiles][4];
 #pragma unroll
@@ -153,80 +411,65 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nsteps = K / BK;
-  u32x4 ra[AChunks / 2];   // one half of a step's A chunks in flight
-  u32x4 bw[4];             // packed weight words of the 4 k-slices of a step
-  GroupSZ gz[2];           // groups of k-slices 0-1 and 2-3 (the same group when G >= 128)
-  auto load_a = [&](int step, int half) {
+  // ---- B ring: slot s & 1 holds the packed weight words and the scales/zeros of step s; each
+  // register is reloaded with step s + 2 right after its last read in step s (a step past K
+  // re-reads the last one: in bounds, never used). kLoadsPerStepB loads per step.
+  u32x4 bw[2][4];
+  GroupSZ gz[2][2];
+  auto load_gz = [&](int slot, int step, int h) {
+    const int g = (min(step, nsteps - 1) * BK + 64 * h) / G;
+    gz[slot][h].s = *reinterpret_cast<const u32x2*>(bs + (int64_t)g * NOUT);
+    gz[slot][h].z = (uint32_t)bz[(int64_t)g * (NOUT / 8)];
+  };
+  auto load_bw = [&](int slot, int step, int kk) {
+    bw[slot][kk] = ld128(bq + (int64_t)(min(step, nsteps - 1) * 16 + kk * 4) * NOUT);
+  };
+  auto load_b = [&](int slot, int step) {
+    load_gz(slot, step, 0);
 #pragma unroll
-    for (int i = 0; i < AChunks / 2; ++i)
-      ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            a_rsrc, a_off[half * (AChunks / 2) + i] + step * BK * 2,
-                                            0, 0));
+    for (int kk = 0; kk < 4; ++kk) load_bw(slot, step, kk);
+    load_gz(slot, step, 1);
   };
-  auto store_a = [&](uint16_t* la, int half) {
-#pragma unroll
-    for (int i = 0; i < AChunks / 2; ++i) {
-      const int r = (tid >> 4) + ARowStep * (half * (AChunks / 2) + i);
-      *reinterpret_cast<u32x4*>(&la[r * LDS_STRIDE + a_kc * 8]) = ra[i];
-    }
-  };
-  auto load_gz = [&](int step, int h) {
-    const int g = (step * BK + 64 * h) / G;
-    gz[h].s = *reinterpret_cast<const u32x2*>(bs + (int64_t)g * NOUT);
-    gz[h].z = (uint32_t)bz[(int64_t)g * (NOUT / 8)];
-  };
-  auto load_bw = [&](int step, int kk) {
-    bw[kk] = ld128(bq + (int64_t)(step * 16 + kk * 4) * NOUT);
-  };
-  load_gz(0, 0);
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) load_bw(0, kk);
-  load_gz(0, 1);
-  load_a(0, 0);
-  store_a(lds_a[0], 0);
-  load_a(0, 1);
-  store_a(lds_a[0], 1);
 
-  for (int step = 0; step < nsteps; ++step) {
-    // Loads for the next step reuse each register right after its last read; on the last step
-    // they re-read the last step (in bounds, never used). The next step's A tile goes to the
-    // other buffer, whose readers (the previous step) all passed this step's barrier.
-    const int nxt = min(step + 1, nsteps - 1);
-    const uint16_t* la = lds_a[step & 1];
-    uint16_t* la_next = lds_a[(step + 1) & 1];
-    __syncthreads();
-
+  // Pipeline: A of step s + 1 is loaded into LDS during step s, B of step s + 2 into registers.
+  // The wait at the top of a step is for this wave's A loads of that step only: the
+  // kLoadsPerStepB B loads issued after them stay in flight.
+  dma_a(lds_a0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_b(0, 0);
+  __builtin_amdgcn_sched_barrier(0);  // issue order = step order
+  load_b(1, 1);
+  const int mtu = __builtin_amdgcn_readfirstlane(mtiles);
+  auto run_step = [&](auto xc, int step) {
+    constexpr int X = decltype(xc)::value;  // step & 1: LDS buffer and B slot
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerStepB));
+    __syncthreads();  // every wave's A of this step landed; the other buffer is free
+    dma_a(X ? lds_a0 : lds_a1, step + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* la = X ? lds_a1 : lds_a0;
     _Float16 sc[4];
     float cc[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if ((kk & 1) == 0) {
-        // fp16 scales and c = -(1024 + z) * s of the lane's 4 columns for this half-step
-        const GroupSZ q = gz[kk >> 1];
-        const uint32_t zw = q.z >> zsh;
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          sc[n] = __builtin_bit_cast(_Float16, (uint16_t)(q.s[n >> 1] >> (16 * (n & 1))));
-          cc[n] = -(1024.0f + (float)((zw >> (4 * n)) & 0xFu)) * (float)sc[n];
-        }
-        load_gz(nxt, kk >> 1);
-        if (kk == 2) store_a(la_next, 0);
-        load_a(nxt, kk >> 1);
+        group_coeffs(gz[X][kk >> 1], zsh, sc, cc);
+        load_gz(X, step + 2, kk >> 1);
       }
       bf16x8_v bfr[4];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) bfr[n] = dequant8_exact(bw[kk][n], sc[n], cc[n]);
-      load_bw(nxt, kk);
-      // A fragments one subtile ahead (a read past mtiles stays inside the buffer, unused)
-      const uint16_t* lrow = &la[j * LDS_STRIDE + kk * 32 + 8 * kq];
+      for (int n = 0; n < 4; ++n) bfr[n] = dequant8_exact(bw[X][kk][n], sc[n], cc[n]);
+      load_bw(X, step + 2, kk);
+      // A fragment of row mi*16 + j at logical chunk 4 kk + kq, one subtile ahead (a read past
+      // mtiles stays inside the buffer, unused)
+      const uint16_t* lrow = la + j * BK + 8 * ((4 * kk + kq) ^ j);
       bf16x8_v af_next = *reinterpret_cast<const bf16x8_v*>(lrow);
 #pragma unroll
       for (int mi = 0; mi < kMTiles; ++mi) {
-        if (mi >= mtiles) break;
+        if (mi >= mtu) break;
         const bf16x8_v af = af_next;
         if (mi + 1 < kMTiles)
-          af_next = *reinterpret_cast<const bf16x8_v*>(lrow + (mi + 1) * 16 * LDS_STRIDE);
+          af_next = *reinterpret_cast<const bf16x8_v*>(lrow + (mi + 1) * 16 * BK);
 #pragma unroll
         for (int n = 0; n < 4; ++n)
           acc[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[n], acc[mi][n], 0, 0, 0);
@@ -234,47 +477,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // ... before these 4 MFMAs
       }
     }
-    store_a(la_next, 1);
+  };
+  for (int step = 0; step < nsteps; step += 2) {  // nsteps is even
+    run_step(std::integral_constant<int, 0>{}, step);
+    run_step(std::integral_constant<int, 1>{}, step + 1);
   }
 
-  // ---- epilogue. D[i][jj] of a 16x16 tile sits in lane jj + 16*(i/4), element i%4; column jj
-  // of tile n is projection column col(jj) + n.
-#pragma unroll
-  for (int mi = 0; mi < kMTiles; ++mi) {
-    if (mi >= mtiles) break;
-#pragma unroll
-    for (int el = 0; el < 4; ++el) {
-      const int r = mi * 16 + 4 * kq + el;
-      const int f = s_slot[r];
-      if (MODE == MODE_W1) {
-        float hv[4];
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const float g = acc[mi][n][el];
-          // lanes jj < 8 hold gate, lane jj + 8 the up value of the same column (row_ror:8)
-          const float u = __int_as_float(
-              __builtin_amdgcn_update_dpp(0, __float_as_int(g), 0x128, 0xF, 0xF, false));
-          hv[n] = silu_f32(g) * u;
-        }
-        if (j < 8 && (unsigned)f < (unsigned)sd.num_slots) {
-          const u32x2 o = {pk_bf16(hv[0], hv[1]), pk_bf16(hv[2], hv[3])};
-          *reinterpret_cast<u32x2*>(&h_out[(int64_t)f * I + col]) = o;
-        }
-      } else {
-        if ((unsigned)f < (unsigned)sd.num_slots) {
-          const float w = topk_w[f];
-          const f32x4 o = {w * acc[mi][0][el], w * acc[mi][1][el], w * acc[mi][2][el],
-                           w * acc[mi][3][el]};
-          if constexpr (YS16) {
-            const u32x2 ob = {pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3])};
-            *reinterpret_cast<u32x2*>(&static_cast<uint16_t*>(ys)[(int64_t)f * H + col]) = ob;
-          } else {
-            *reinterpret_cast<f32x4*>(&static_cast<float*>(ys)[(int64_t)f * H + col]) = o;
-          }
-        }
-      }
-    }
-  }
+  block_epilogue<MODE, YS16>(acc, mtiles, s_slot, j, kq, col, sd.num_slots, I, H, s_w, h_out,
+                             ys);
 }
 
 // Workgroups for up to `items` items, a multiple of 8 (each XCD gets the same number).
