@@ -79,10 +79,61 @@ __global__ __launch_bounds__(64) void align_chunk_kernel(const int32_t* __restri
   for (int g = lane; g < G; g += 64) scratch[n_slots + c * G + g] = cnt[g];
 }
 
+// Block order for the grouped GEMMs, heaviest first: border[r] = the r-th align block sorted by
+// its number of 16-row subtiles holding slots (class BM/16 first, down to 1), ties in block
+// order. Big blocks then start in the first wave of workgroups and the light ones fill the tail.
+// One wave: lane l owns groups [l per, (l + 1) per); per class, an exclusive scan over lanes
+// gives each lane's first position. An expert's blocks are all full except the last.
+constexpr int kOrderMaxClasses = 8;  // BM <= 128
+// Subtiles holding slots in the last block of a group of n > 0 slots.
+MOE_DEV int last_class(int n, int BM) { return (n - (n - 1) / BM * BM + 15) / 16; }
+MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, int BM, int lane,
+                         int32_t* __restrict__ border) {
+  const int NC = BM / 16;
+  const int per = (G + 63) / 64;
+  const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
+  int cnt[kOrderMaxClasses];  // cnt[c]: this lane's blocks of class c + 1
+#pragma unroll
+  for (int c = 0; c < kOrderMaxClasses; ++c) cnt[c] = 0;
+  for (int g = g0; g < g1; ++g) {
+    const int n = s_cnt[g];
+    if (n == 0) continue;
+    const int lc = last_class(n, BM);
+#pragma unroll
+    for (int c = 0; c < kOrderMaxClasses; ++c) {
+      if (c == NC - 1) cnt[c] += (n - 1) / BM;  // the full blocks before the last
+      if (c == lc - 1) cnt[c] += 1;
+    }
+  }
+  int pos[kOrderMaxClasses];  // this lane's next position per class
+  int base = 0;
+#pragma unroll
+  for (int c = kOrderMaxClasses - 1; c >= 0; --c) {  // classes heaviest first
+    int incl = cnt[c];
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    pos[c] = base + incl - cnt[c];
+    base += __shfl(incl, 63, 64);
+  }
+  for (int g = g0; g < g1; ++g) {
+    const int n = s_cnt[g];
+    if (n == 0) continue;
+    const int b0 = s_off[g] / BM, nb = (n + BM - 1) / BM, lc = last_class(n, BM);
+#pragma unroll
+    for (int c = 0; c < kOrderMaxClasses; ++c) {
+      if (c == NC - 1)
+        for (int j = 0; j < nb - 1; ++j) border[pos[c]++] = b0 + j;
+      if (c == lc - 1) border[pos[c]++] = b0 + nb - 1;
+    }
+  }
+}
+
 __global__ __launch_bounds__(1024) void align_finish_kernel(
     const int32_t* __restrict__ topk_ids, int T, int top_k, int E, int has_shared, int BM,
     int cap, int CH, int nchunks, int32_t* __restrict__ sorted, int32_t* __restrict__ eids,
-    int32_t* __restrict__ ntpp) {
+    int32_t* __restrict__ ntpp, int32_t* __restrict__ border) {
   __shared__ int cl[kAlign2LdsCounts];  // [chunk][group]: counts, then bases inside the group
   __shared__ int s_off[kMaxGroups], s_pad[kMaxGroups];
   __shared__ int s_total;
@@ -153,6 +204,7 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
   __syncthreads();
   const int tp = s_total;
   const int limit = cap * BM;
+  if (border && w == 0) block_order(s_off, s_pad, G, BM, lane, border);
   // 4. padding sentinels (four threads per group, 16-byte stores) and block ids
   const bool vec = (reinterpret_cast<uintptr_t>(sorted) & 15u) == 0;
   for (int g = tid >> 2; g < G; g += 256) {
@@ -194,25 +246,40 @@ int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM) {
   return bound;
 }
 
-hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
-                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp,
-                        hipStream_t stream) {
+namespace {
+// Chunks of the two-kernel align, or 0 when the input takes the one-block kernel: large inputs
+// with room for the scratch in the sorted buffer.
+int align_chunks(int T, int top_k, int E, int has_shared, int BM, int cap, int* CH) {
   const int n_slots = T * top_k + (has_shared ? T : 0);
   const int G = E + (has_shared ? 1 : 0);
-  // Large inputs with room for the scratch in the sorted buffer: two kernels.
   int nchunks = kAlign2LdsCounts / G;
   if (nchunks > kAlign2MaxChunks) nchunks = kAlign2MaxChunks;
-  const int CH = nchunks > 0 ? ((n_slots + nchunks - 1) / nchunks + 63) / 64 * 64 : 0;
-  if (n_slots >= 4096 && BM >= 64 && nchunks > 0 &&
-      n_slots <= 1024 * kAlign2MaxSlotsPerThread && G <= kMaxGroups &&
-      (int64_t)cap * BM >= (int64_t)n_slots + (int64_t)nchunks * G) {
-    nchunks = (n_slots + CH - 1) / CH;
+  if (n_slots < 4096 || BM < 64 || BM > 16 * kOrderMaxClasses || nchunks <= 0 ||
+      n_slots > 1024 * kAlign2MaxSlotsPerThread || G > kMaxGroups ||
+      (int64_t)cap * BM < (int64_t)n_slots + (int64_t)nchunks * G)
+    return 0;
+  *CH = ((n_slots + nchunks - 1) / nchunks + 63) / 64 * 64;
+  return (n_slots + *CH - 1) / *CH;
+}
+}  // namespace
+
+bool align_orders_blocks(int T, int top_k, int E, int has_shared, int BM, int cap) {
+  int CH = 0;
+  return align_chunks(T, top_k, E, has_shared, BM, cap, &CH) > 0;
+}
+
+hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
+                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
+                        hipStream_t stream) {
+  int CH = 0;
+  const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, &CH);
+  if (nchunks > 0) {
     hipLaunchKernelGGL(align_chunk_kernel, dim3(nchunks), dim3(64), 0, stream, topk_ids, T,
                        top_k, E, has_shared, CH, sorted);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(align_finish_kernel, dim3(1), dim3(1024), 0, stream, topk_ids, T, top_k, E,
-                       has_shared, BM, cap, CH, nchunks, sorted, eids, ntpp);
+                       has_shared, BM, cap, CH, nchunks, sorted, eids, ntpp, border);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, topk_ids, T, top_k, E,

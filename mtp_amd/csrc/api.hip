@@ -94,18 +94,20 @@ int resolve_path(int path, int T, int top_k) {
 int block_m_of(int path) { return path == MOE_PATH_PREFILL ? kPrefillBlockM : kDecodeBlockM; }
 
 hipError_t dispatch_w1(int path, const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
-                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int bm,
-                       int cap, uint16_t* h, hipStream_t s) {
-  if (path == MOE_PATH_PREFILL) return launch_w1_prefill(x, ed, sd, sorted, eids, ntpp, bm, cap, h, s);
+                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                       const int32_t* border, int bm, int cap, uint16_t* h, hipStream_t s) {
+  if (path == MOE_PATH_PREFILL)
+    return launch_w1_prefill(x, ed, sd, sorted, eids, ntpp, border, bm, cap, h, s);
   if (path == MOE_PATH_GEMV) return launch_w1_decode(x, ed, sd, sorted, eids, ntpp, bm, cap, h, s);
   return launch_w1_decode_mfma(x, ed, sd, sorted, eids, ntpp, cap, h, s);
 }
 
 hipError_t dispatch_w2(int path, const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
-                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp, int bm,
-                       int cap, const float* w, float* ys, hipStream_t s) {
+                       const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
+                       const int32_t* border, int bm, int cap, const float* w, float* ys,
+                       hipStream_t s) {
   if (path == MOE_PATH_PREFILL)
-    return launch_w2_prefill(h, ed, sd, sorted, eids, ntpp, bm, cap, w, ys, s);
+    return launch_w2_prefill(h, ed, sd, sorted, eids, ntpp, border, bm, cap, w, ys, s);
   if (path == MOE_PATH_GEMV) return launch_w2_decode(h, ed, sd, sorted, eids, ntpp, bm, cap, w, ys, s);
   return launch_w2_decode_mfma(h, ed, sd, sorted, eids, ntpp, cap, w, ys, s);
 }
@@ -114,7 +116,7 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Workspace of moe_layer_v1 / moe_fused_experts_v1 (no state survives between calls).
 struct Workspace {
-  size_t logits, ids, w, sorted, eids, ntpp, h, ys, total;
+  size_t logits, ids, w, sorted, eids, ntpp, border, h, ys, total;
   int cap, bm;
 };
 
@@ -131,6 +133,7 @@ Workspace layout(int T, int top_k, const moe_expert_set_v1* ex, int has_shared, 
   L.sorted = o; o += align256((size_t)L.cap * L.bm * 4);
   L.eids = o;   o += align256((size_t)L.cap * 4);
   L.ntpp = o;   o += 256;
+  L.border = o; o += align256((size_t)L.cap * 4);  // block order of the large-input align
   L.h = o;      o += align256(slots * I * 2);
   L.ys = o;     o += align256(slots * H * 4);
   L.total = o;
@@ -162,6 +165,11 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   int32_t* ntpp = at<int32_t>(ws, L.ntpp);
   uint16_t* h = at<uint16_t>(ws, L.h);
   float* ys = at<float>(ws, L.ys);
+  // the large-input align also orders the blocks for the prefill GEMMs
+  int32_t* border = routing == ROUTE_ALIGN && path == MOE_PATH_PREFILL &&
+                            align_orders_blocks(T, top_k, ex->num_experts, has_shared, L.bm, L.cap)
+                        ? at<int32_t>(ws, L.border)
+                        : nullptr;
   const bool grid = routing == ROUTE_GRID_LOGITS || routing == ROUTE_GRID_IDS;
   if (grid) {
     const SlotGrid sg{1, routing == ROUTE_GRID_LOGITS ? at<float>(ws, L.logits) : nullptr, ids, w};
@@ -169,8 +177,9 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   } else {
     if (routing == ROUTE_ALIGN)
       MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
-                                 eids, ntpp, stream), "align");
-    MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, L.bm, L.cap, h, stream), "w1");
+                                 eids, ntpp, border, stream), "align");
+    MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, border, L.bm, L.cap, h, stream),
+                  "w1");
   }
   if (path == MOE_PATH_DECODE && w2_token_sum_fits(ed, sd)) {
     MOE_CHECK_HIP(launch_w2_token_sum(h, ed, sd, ids, w, out, stream), "w2 + sum");
@@ -178,7 +187,7 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   }
   if (path == MOE_PATH_PREFILL) {  // bf16 slot rows: half the rows' HBM traffic
     uint16_t* ys16 = at<uint16_t>(ws, L.ys);
-    MOE_CHECK_HIP(launch_w2_prefill_bf16(h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys16,
+    MOE_CHECK_HIP(launch_w2_prefill_bf16(h, ed, sd, sorted, eids, ntpp, border, L.bm, L.cap, w, ys16,
                                          stream), "w2");
     MOE_CHECK_HIP(launch_moe_sum_bf16(ys16, T, top_k, ex->hidden, has_shared, ids,
                                       ex->num_experts, ex->expert_row, out, stream),
@@ -189,7 +198,8 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
     MOE_CHECK_HIP(launch_w2_decode_slotgrid(h, ed, sd, SlotGrid{1, nullptr, ids, w}, ys, stream),
                   "w2 (slot grid)");
   else
-    MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, L.bm, L.cap, w, ys, stream),
+    MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted, eids, ntpp, nullptr, L.bm, L.cap, w, ys,
+                              stream),
                   "w2");
   MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, ids, ex->num_experts,
                                ex->expert_row, out, stream),
@@ -306,7 +316,8 @@ int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_
     return fail(MOE_ERR_WORKSPACE, "align: capacity_blocks=%d < required %d", capacity_blocks,
                 need);
   MOE_CHECK_HIP(launch_align(topk_ids, T, top_k, num_experts, has_shared ? 1 : 0, block_m,
-                             capacity_blocks, sorted_ids, expert_ids, ntpp, (hipStream_t)stream),
+                             capacity_blocks, sorted_ids, expert_ids, ntpp, nullptr,
+                             (hipStream_t)stream),
                 "align");
   return MOE_OK;
 }
@@ -327,7 +338,7 @@ int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
                 block_m_of(path));
   const ExpertsDev ed = make_experts_dev(experts, shared);
   const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
-  MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+  MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted_ids, expert_ids, ntpp, nullptr, block_m,
                             capacity_blocks, h, (hipStream_t)stream), "w1");
   return MOE_OK;
 }
@@ -349,7 +360,7 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
                 block_m_of(path));
   const ExpertsDev ed = make_experts_dev(experts, shared);
   const SlotsDev sd{T, top_k, T * top_k + (shared ? T : 0)};
-  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted_ids, expert_ids, ntpp, block_m,
+  MOE_CHECK_HIP(dispatch_w2(path, h, ed, sd, sorted_ids, expert_ids, ntpp, nullptr, block_m,
                             capacity_blocks, topk_weights, ys,
                             (hipStream_t)stream), "w2");
   return MOE_OK;

@@ -265,8 +265,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
     const uint16_t* __restrict__ A,  // W1: x [T, H]; W2: h [num_slots, I]
     ExpertsDev ed, SlotsDev sd, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ eids, const int32_t* __restrict__ ntpp,
-    const float* __restrict__ topk_w, uint16_t* __restrict__ h_out, void* __restrict__ ys,
-    int a_bytes, int ncolblk) {
+    const int32_t* __restrict__ border, const float* __restrict__ topk_w,
+    uint16_t* __restrict__ h_out, void* __restrict__ ys, int a_bytes, int ncolblk) {
   // Two A buffers as separate objects: the compiler then knows that reads of one do not wait
   // for the LDS loads in flight into the other.
   __shared__ __attribute__((aligned(16))) uint16_t lds_a0[BM * BK];
@@ -274,17 +274,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   __shared__ int s_slot[BM];
   __shared__ float s_w[MODE == MODE_W2 ? BM : 1];  // routed weight of each row (W2)
 
-  // XCD-aware order: workgroup p runs on XCD p % 8, and XCD c takes the contiguous range
-  // [c S, c S + S) of the used (align block, column block) items, numbered expert-major, so the
-  // column blocks of one align block (same A rows) run back to back on one XCD and share the
-  // rows in its L2. (Dealing whole blocks to the XCDs in turn evens out their work - a few hot
-  // experts' full blocks otherwise land on some XCDs - but measured no faster.)
-  const int used = (*ntpp / BM) * ncolblk;
-  const int per_xcd = (used + 7) / 8;
-  const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
-  if ((int)(blockIdx.x >> 3) >= per_xcd || logical >= used) return;
-  const int b = logical / ncolblk;  // align block
-  const int cblk = logical % ncolblk;
+  // XCD-aware order: workgroup p runs on XCD p % 8 and each XCD runs the column blocks of one
+  // align block back to back, so they share the block's A rows in that XCD's L2.
+  //  - With a block order (border, heaviest first), the ordered blocks are dealt to the XCDs in
+  //    turn: every XCD starts on its share of the big blocks and ends on light ones.
+  //  - Without one, XCD c takes the contiguous range [c S, c S + S) of the (block, column block)
+  //    items, numbered expert-major.
+  const int nblk = *ntpp / BM;
+  int b, cblk;
+  if (border) {
+    const int q = (int)(blockIdx.x >> 3);
+    const int r = (q / ncolblk) * 8 + (int)(blockIdx.x & 7);
+    if (r >= nblk) return;
+    b = border[r];
+    cblk = q % ncolblk;
+  } else {
+    const int used = nblk * ncolblk;
+    const int per_xcd = (used + 7) / 8;
+    const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    if ((int)(blockIdx.x >> 3) >= per_xcd || logical >= used) return;
+    b = logical / ncolblk;
+    cblk = logical % ncolblk;
+  }
   const int e = eids[b];
   if (!expert_ok(ed, e)) return;
 
@@ -487,8 +498,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
                              ys);
 }
 
-// Workgroups for up to `items` items, a multiple of 8 (each XCD gets the same number).
-int xcd_grid(int items) { return ((items + 7) / 8) * 8; }
+// Workgroups for up to `cap` align blocks x ncb column blocks in either order: eight XCD shares
+// of ceil(cap / 8) blocks (at least ceil(cap ncb / 8) items each).
+int xcd_grid(int cap, int ncb) { return ((cap + 7) / 8) * 8 * ncb; }
 
 }  // namespace
 
@@ -498,15 +510,16 @@ int xcd_grid(int items) { return ((items + 7) / 8) * 8; }
 // A tile over twice the columns (W1 160 vs 179 us at T = 2048), which leaves one workgroup per CU.
 hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                             int BMr, int cap, uint16_t* h, hipStream_t stream) {
+                             const int32_t* border, int BMr, int cap, uint16_t* h,
+                             hipStream_t stream) {
   const int64_t a_bytes = (int64_t)sd.T * ed.hidden * 2;  // x [T, H] bf16
   if (BMr != BM || ed.hidden % BK != 0 || ed.inter % 128 != 0 || ed.group < 64 ||
       a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
   const int ncb = ed.inter / 128;
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W1, false, 4>), dim3(xcd_grid(cap * ncb)),
-                     dim3(256), 0, stream, x, ed, sd, sorted, eids, ntpp, (const float*)nullptr, h,
-                     (void*)nullptr, (int)a_bytes, ncb);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W1, false, 4>), dim3(xcd_grid(cap, ncb)),
+                     dim3(256), 0, stream, x, ed, sd, sorted, eids, ntpp, border,
+                     (const float*)nullptr, h, (void*)nullptr, (int)a_bytes, ncb);
   return hipGetLastError();
 }
 
@@ -514,15 +527,15 @@ namespace {
 template <bool YS16>
 hipError_t launch_w2_prefill_t(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                               int BMr, int cap, const float* topk_w, void* ys,
-                               hipStream_t stream) {
+                               const int32_t* border, int BMr, int cap, const float* topk_w,
+                               void* ys, hipStream_t stream) {
   const int64_t a_bytes = (int64_t)sd.num_slots * ed.inter * 2;  // h [num_slots, I] bf16
   if (BMr != BM || ed.inter % BK != 0 || ed.hidden % 256 != 0 || ed.group < 64 ||
       a_bytes >= kOutOfRange)
     return hipErrorInvalidValue;
   const int ncb = ed.hidden / 256;
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W2, YS16, 4>), dim3(xcd_grid(cap * ncb)),
-                     dim3(256), 0, stream, h, ed, sd, sorted, eids, ntpp, topk_w,
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_W2, YS16, 4>), dim3(xcd_grid(cap, ncb)),
+                     dim3(256), 0, stream, h, ed, sd, sorted, eids, ntpp, border, topk_w,
                      (uint16_t*)nullptr, ys, (int)a_bytes, ncb);
   return hipGetLastError();
 }
@@ -530,14 +543,16 @@ hipError_t launch_w2_prefill_t(const uint16_t* h, const ExpertsDev& ed, const Sl
 
 hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                             int BMr, int cap, const float* topk_w, float* ys,
-                             hipStream_t stream) {
-  return launch_w2_prefill_t<false>(h, ed, sd, sorted, eids, ntpp, BMr, cap, topk_w, ys, stream);
+                             const int32_t* border, int BMr, int cap, const float* topk_w,
+                             float* ys, hipStream_t stream) {
+  return launch_w2_prefill_t<false>(h, ed, sd, sorted, eids, ntpp, border, BMr, cap, topk_w, ys,
+                                    stream);
 }
 
 hipError_t launch_w2_prefill_bf16(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                   const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                                  int BMr, int cap, const float* topk_w, uint16_t* ys,
-                                  hipStream_t stream) {
-  return launch_w2_prefill_t<true>(h, ed, sd, sorted, eids, ntpp, BMr, cap, topk_w, ys, stream);
+                                  const int32_t* border, int BMr, int cap, const float* topk_w,
+                                  uint16_t* ys, hipStream_t stream) {
+  return launch_w2_prefill_t<true>(h, ed, sd, sorted, eids, ntpp, border, BMr, cap, topk_w, ys,
+                                   stream);
 }

@@ -35,8 +35,11 @@ hipError_t launch_shared_gate(const uint16_t* x, int T, int H, const uint16_t* s
                               int top_k, float* logits_ws, float* weights, hipStream_t stream);
 
 int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM);
+// Whether launch_align writes `border` for these sizes (the large-input path): the align blocks
+// sorted by the number of 16-row subtiles holding slots, heaviest first (cap entries at most).
+bool align_orders_blocks(int T, int top_k, int E, int has_shared, int BM, int cap);
 hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
-                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp,
+                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
                         hipStream_t stream);
 
 // Slot-grid routing for decode-size batches (slot_grid_fits): the MFMA decode kernels take their
@@ -93,18 +96,20 @@ hipError_t launch_w2_token_sum(const uint16_t* h, const ExpertsDev& ed, const Sl
                                const int32_t* ids, const float* topk_w, uint16_t* out,
                                hipStream_t stream);
 
-// Prefill (bf16 MFMA) path.
+// Prefill (bf16 MFMA) path. border (nullable): the block order of align_orders_blocks.
 hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                             int BM, int cap, uint16_t* h, hipStream_t stream);
+                             const int32_t* border, int BM, int cap, uint16_t* h,
+                             hipStream_t stream);
 hipError_t launch_w2_prefill(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                             int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
+                             const int32_t* border, int BM, int cap, const float* topk_w,
+                             float* ys, hipStream_t stream);
 // The same with bf16 slot rows (the fused layer's workspace; halves the rows' HBM traffic).
 hipError_t launch_w2_prefill_bf16(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                   const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                                  int BM, int cap, const float* topk_w, uint16_t* ys,
-                                  hipStream_t stream);
+                                  const int32_t* border, int BM, int cap, const float* topk_w,
+                                  uint16_t* ys, hipStream_t stream);
 
 // Predictor MLP with L heads: z1 = h . w1^T over all L*D rows (fp32 [T][L*D+1]),
 // a = bf16(silu(z1)) head-major [L][T][D], z2[l] = a[l] . w2[l]^T (fp32 [L][T][E+1]),

@@ -60,10 +60,12 @@ def test_config1_full_shape(T, path):
 
 @pytest.mark.parametrize("E,H,I,G,T,shared", [(32, 1024, 1024, 64, 200, True),
                                                (16, 1536, 512, 256, 130, False),
-                                               (24, 512, 256, 128, 300, True)])
+                                               (24, 512, 256, 128, 300, True),
+                                               (24, 512, 256, 128, 1100, True)])
 def test_prefill_shapes_and_groups(E, H, I, G, T, shared):
     """Prefill GEMMs over other hidden / intermediate sizes, group sizes 64 and 256, with and
-    without the shared expert (its block reads the shared projections)."""
+    without the shared expert (its block reads the shared projections). T = 1100 (5500 slots)
+    takes the large-input align, which also orders the blocks heaviest first for the GEMMs."""
     _say(f"prefill shape E={E} H={H} I={I} G={G} T={T} shared={shared}")
     layer = synth.make_layer(3, num_experts=E, hidden=H, intermediate=I, zipf=True, shared=shared,
                              group=G)
