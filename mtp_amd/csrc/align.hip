@@ -237,6 +237,124 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
   }
 }
 
+// Kernel 2 of the scratch form (fused layer calls, whose workspace holds the ranks and counts
+// outside the output buffers): one 1024-thread workgroup per chunk. Every workgroup reads all
+// chunk counts, derives the group sizes, the group offsets (exclusive scan of padded sizes) and
+// its own chunk's base inside each group, and writes the slots of its chunk at
+// offset + chunk base + rank. The groups' padding sentinels and block ids are dealt to the
+// workgroups in turn; one extra workgroup (blockIdx nchunks) writes ntpp and the block order. The layout is the one of
+// align_finish_kernel, but the 4-byte slot stores come from nchunks CUs instead of one, and each
+// group's chunk counts are summed by four threads with independent reads instead of walked
+// serially.
+__global__ __launch_bounds__(1024) void align_scatter_kernel(
+    const int32_t* __restrict__ topk_ids, int T, int top_k, int E, int has_shared, int BM,
+    int cap, int CH, int nchunks, const int32_t* __restrict__ scratch,
+    int32_t* __restrict__ sorted, int32_t* __restrict__ eids, int32_t* __restrict__ ntpp,
+    int32_t* __restrict__ border) {
+  __shared__ int cl[kAlign2LdsCounts];  // [chunk][group] counts
+  __shared__ int s_off[kMaxGroups], s_cnt[kMaxGroups], s_pre[kMaxGroups];
+  __shared__ int s_total;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = blockIdx.x;
+  const int routed = T * top_k;
+  const int n_slots = routed + (has_shared ? T : 0);
+  const int G = E + (has_shared ? 1 : 0);
+  const int ncnt = nchunks * G;
+  // 1. all counts (16 loads per thread in flight together) and this thread's first slot of the
+  //    chunk (its rank and raw id)
+  {
+    constexpr int NL = (kAlign2LdsCounts + 1023) / 1024;
+    const __amdgpu_buffer_rsrc_t cr = buf_rsrc(scratch + n_slots, (uint32_t)ncnt * 4u);
+    int v[NL];
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int i = tid + 1024 * k;
+      v[k] = (int)buf_ld32(cr, i < ncnt ? (uint32_t)i * 4u : kOutOfRange);
+    }
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int i = tid + 1024 * k;
+      if (i < kAlign2LdsCounts) cl[i] = v[k];
+    }
+  }
+  const int lo = min(c * CH, n_slots), hi = min(lo + CH, n_slots);
+  const __amdgpu_buffer_rsrc_t ir = buf_rsrc(topk_ids, (uint32_t)routed * 4u);
+  const __amdgpu_buffer_rsrc_t rr = buf_rsrc(scratch, (uint32_t)n_slots * 4u);
+  const int f0 = lo + tid;
+  const int rk0 = (int)buf_ld32(rr, f0 < hi ? (uint32_t)f0 * 4u : kOutOfRange);
+  const int raw0 = (int)buf_ld32(ir, f0 < hi && f0 < routed ? (uint32_t)f0 * 4u : kOutOfRange);
+  __syncthreads();
+  // 2. per group: its slot count and the slots of the chunks before this one. Four adjacent
+  //    threads per group each sum 16 chunks (independent LDS reads, unrolled), then the quad
+  //    combines its partial sums.
+  static_assert(kAlign2MaxChunks == 64, "four parts of 16 chunks");
+  for (int i = tid; i < G * 4; i += 1024) {
+    const int g = i >> 2, part = i & 3;
+    int tot = 0, pre = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int q = part * 16 + j;
+      const int n = cl[q < nchunks ? q * G + g : 0];
+      tot += q < nchunks ? n : 0;
+      pre += q < c ? n : 0;
+    }
+    tot += __shfl_xor(tot, 1, 64);
+    pre += __shfl_xor(pre, 1, 64);
+    tot += __shfl_xor(tot, 2, 64);
+    pre += __shfl_xor(pre, 2, 64);
+    if (part == 0) {
+      s_cnt[g] = tot;
+      s_pre[g] = pre;
+    }
+  }
+  __syncthreads();
+  // 3. group offsets: exclusive scan of the padded sizes by one wave
+  if (w == 0) {
+    const int per = (G + 63) / 64;
+    const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
+    int local = 0;
+    for (int g = g0; g < g1; ++g) local += (s_cnt[g] + BM - 1) / BM * BM;
+    int incl = local;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    int run = incl - local;
+    for (int g = g0; g < g1; ++g) {
+      s_off[g] = run;
+      run += (s_cnt[g] + BM - 1) / BM * BM;
+    }
+    if (lane == 63) s_total = incl;
+  }
+  __syncthreads();
+  const int tp = s_total;
+  const int limit = cap * BM;
+  // 4. this workgroup's share of the layout: groups c, c + nchunks, ... (padding sentinels and
+  //    block ids), a stride of the tail past the padded total, ntpp and the block order
+  if (c == nchunks) {  // the extra workgroup: ntpp and the block order only
+    if (tid == 0) *ntpp = tp;
+    if (border && w == 0) block_order(s_off, s_cnt, G, BM, lane, border);
+    return;
+  }
+  for (int g = c; g < G; g += nchunks) {
+    const int off = s_off[g], real_end = off + s_cnt[g];
+    const int end = min(g + 1 < G ? s_off[g + 1] : tp, limit);
+    for (int p = real_end + tid; p < end; p += 1024) sorted[p] = n_slots;
+    for (int b = off / BM + tid; b < end / BM; b += 1024) eids[b] = g;
+  }
+  for (int b = tp / BM + c * 1024 + tid; b < cap; b += nchunks * 1024) eids[b] = -1;
+  for (int p = tp + c * 1024 + tid; p < limit; p += nchunks * 1024) sorted[p] = n_slots;
+  // 5. the slots of this chunk
+  for (int f = f0; f < hi; f += 1024) {
+    const int rk = f == f0 ? rk0 : scratch[f];
+    const int raw = f == f0 ? raw0 : (f < routed ? topk_ids[f] : 0);
+    const int e = f < routed ? ((raw >= 0 && raw < E) ? raw : -1) : E;
+    if (e >= 0) {
+      const int pos = s_off[e] + s_pre[e] + rk;
+      if (pos < limit) sorted[pos] = f;
+    }
+  }
+}
+
 }  // namespace
 
 int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM) {
@@ -268,11 +386,29 @@ bool align_orders_blocks(int T, int top_k, int E, int has_shared, int BM, int ca
   return align_chunks(T, top_k, E, has_shared, BM, cap, &CH) > 0;
 }
 
-hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
-                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
-                        hipStream_t stream) {
+int64_t align_scratch_bytes(int T, int top_k, int E, int has_shared, int BM, int cap) {
   int CH = 0;
   const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, &CH);
+  if (nchunks <= 0) return 0;
+  const int64_t n_slots = (int64_t)T * top_k + (has_shared ? T : 0);
+  return (n_slots + (int64_t)nchunks * (E + (has_shared ? 1 : 0))) * 4;
+}
+
+hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
+                        int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
+                        int32_t* scratch, hipStream_t stream) {
+  int CH = 0;
+  const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, &CH);
+  if (nchunks > 0 && scratch) {
+    hipLaunchKernelGGL(align_chunk_kernel, dim3(nchunks), dim3(64), 0, stream, topk_ids, T,
+                       top_k, E, has_shared, CH, scratch);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(align_scatter_kernel, dim3(nchunks + 1), dim3(1024), 0, stream, topk_ids, T,
+                       top_k, E, has_shared, BM, cap, CH, nchunks, scratch, sorted, eids, ntpp,
+                       border);
+    return hipGetLastError();
+  }
   if (nchunks > 0) {
     hipLaunchKernelGGL(align_chunk_kernel, dim3(nchunks), dim3(64), 0, stream, topk_ids, T,
                        top_k, E, has_shared, CH, sorted);

@@ -175,9 +175,17 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
     const SlotGrid sg{1, routing == ROUTE_GRID_LOGITS ? at<float>(ws, L.logits) : nullptr, ids, w};
     MOE_CHECK_HIP(launch_w1_decode_slotgrid(x, ed, sd, sg, h, stream), "w1 (slot grid)");
   } else {
-    if (routing == ROUTE_ALIGN)
+    if (routing == ROUTE_ALIGN) {
+      // the ys section is not in use until W2: the large-input align keeps its ranks and
+      // chunk counts there
+      const int64_t scratch_bytes =
+          align_scratch_bytes(T, top_k, ex->num_experts, has_shared, L.bm, L.cap);
+      int32_t* scratch = scratch_bytes > 0 && (size_t)scratch_bytes <= L.total - L.ys
+                             ? at<int32_t>(ws, L.ys)
+                             : nullptr;
       MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
-                                 eids, ntpp, border, stream), "align");
+                                 eids, ntpp, border, scratch, stream), "align");
+    }
     MOE_CHECK_HIP(dispatch_w1(path, x, ed, sd, sorted, eids, ntpp, border, L.bm, L.cap, h, stream),
                   "w1");
   }
@@ -316,7 +324,7 @@ int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_
     return fail(MOE_ERR_WORKSPACE, "align: capacity_blocks=%d < required %d", capacity_blocks,
                 need);
   MOE_CHECK_HIP(launch_align(topk_ids, T, top_k, num_experts, has_shared ? 1 : 0, block_m,
-                             capacity_blocks, sorted_ids, expert_ids, ntpp, nullptr,
+                             capacity_blocks, sorted_ids, expert_ids, ntpp, nullptr, nullptr,
                              (hipStream_t)stream),
                 "align");
   return MOE_OK;

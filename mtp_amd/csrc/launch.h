@@ -38,9 +38,13 @@ int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM);
 // Whether launch_align writes `border` for these sizes (the large-input path): the align blocks
 // sorted by the number of 16-row subtiles holding slots, heaviest first (cap entries at most).
 bool align_orders_blocks(int T, int top_k, int E, int has_shared, int BM, int cap);
+// Bytes of scratch (outside the output buffers) that lets launch_align spread the large-input
+// scatter over many workgroups; 0 when these sizes take the one-block kernel.
+int64_t align_scratch_bytes(int T, int top_k, int E, int has_shared, int BM, int cap);
+// scratch (nullable): align_scratch_bytes bytes the call may overwrite.
 hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
                         int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
-                        hipStream_t stream);
+                        int32_t* scratch, hipStream_t stream);
 
 // Slot-grid routing for decode-size batches (slot_grid_fits): the MFMA decode kernels take their
 // expert and rows from the routed ids themselves instead of an align pass. Workgroup y = slot

@@ -210,3 +210,56 @@ def test_decode_repeated_ids(case):
         err = moe_ref.rel_err(got.float().cpu().numpy(), ref)
         _say(f"  {path}: rel_err={err:.3e}")
         assert np.isfinite(err) and err <= LAYER_RTOL
+
+
+def _workspace_offsets(T, k, E, has_shared, bm, cap):
+    """Byte offsets of the routing sections of a layer workspace, in the library's order
+    (logits, ids, weights, sorted slot ids, block experts, ntpp, block order; each 256-byte
+    aligned)."""
+    def a256(n):
+        return (n + 255) // 256 * 256
+    slots = T * k + (T if has_shared else 0)
+    sizes = (("logits", T * (E + 1) * 4), ("ids", T * k * 4), ("w", slots * 4),
+             ("sorted", cap * bm * 4), ("eids", cap * 4), ("ntpp", 256), ("border", cap * 4))
+    off, out = 0, {}
+    for name, n in sizes:
+        out[name] = off
+        off += a256(n)
+    return out
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_fused_prefill_align_layout(shared):
+    """The fused layer's large-input align (per-chunk ranks, then one workgroup per chunk that
+    derives the group offsets and scatters its own slots) writes the oracle's stable layout, the
+    unused tail, and the block order heaviest first (16-row subtiles holding slots, ties in
+    block order)."""
+    T, k, E, BM = 2048, 8, 256, ops.PREFILL_BLOCK_M
+    _say(f"fused prefill align layout T={T} shared={shared}")
+    layer = to_gpu(synth.make_layer(5, num_experts=E, hidden=512, intermediate=256, zipf=True,
+                                    shared=shared))
+    x = synth.make_tokens(T, 512, seed=13).cuda()
+    need = ops.workspace_bytes(T, k, layer.experts, shared, "prefill")
+    ws = torch.full((need,), 0x5A, dtype=torch.uint8, device="cuda")
+    _, ids, _ = ops.moe_layer(x, layer.router_w, layer.experts, top_k=k,
+                              logit_bias=layer.logit_bias, shared=layer.shared,
+                              shared_gate_w=layer.shared_gate_w, path="prefill", workspace=ws,
+                              return_routing=True)
+    torch.cuda.synchronize()
+    cap = ops.capacity_blocks(T, k, E, shared, BM)
+    o = _workspace_offsets(T, k, E, shared, BM, cap)
+    i32 = ws.view(torch.int32).cpu().numpy()
+    got_sorted = i32[o["sorted"] // 4: o["sorted"] // 4 + cap * BM]
+    got_eids = i32[o["eids"] // 4: o["eids"] // 4 + cap]
+    got_ntpp = int(i32[o["ntpp"] // 4])
+    rs, re_, rn = moe_ref.align_block_padded(ids.cpu().numpy(), E, BM, has_shared=shared,
+                                             capacity_blocks=cap)
+    assert got_ntpp == rn
+    assert np.array_equal(got_sorted, rs)
+    assert np.array_equal(got_eids, re_)
+    n_slots = T * k + (T if shared else 0)
+    nblk = rn // BM
+    cls = [(int((rs[b * BM:(b + 1) * BM] < n_slots).sum()) + 15) // 16 for b in range(nblk)]
+    want = sorted(range(nblk), key=lambda b: (-cls[b], b))
+    got_border = i32[o["border"] // 4: o["border"] // 4 + nblk]
+    assert list(got_border) == want
