@@ -8,10 +8,10 @@
 // r = s*4 + (l >> 4) at columns cl .. cl + CT - 1 with cl = c0 + CT*(l & 15) (one 8- or 16-byte
 // nontemporal load; 16 lanes read 16*CT*4 contiguous bytes of a row). One packed int32 is
 // exactly the 8 k-values one lane contributes to a 16x16x32 MFMA, so each int32 becomes one B
-// fragment: the bf16 "magic" pairs (128 + q_j, 128 + q_{j+4}) give the k order
-// [0,4,1,5,2,6,3,7]; the A fragment (activations) is loaded as 8 consecutive bf16 and permuted
-// to the same order (v_perm), so the dot products are unchanged. N-subtile j of a lane holds
-// column cl + j.
+// fragment: bf16 "magic" pairs 128 + q built from two byte planes of the word (weight_frag)
+// give the k order [0,2,4,6,1,3,5,7]; the A fragment (activations) is loaded as 8 consecutive
+// bf16 and permuted to the same order (v_perm), so the dot products are unchanged. N-subtile j
+// of a lane holds column cl + j.
 //
 // Zero point and scale are applied per quantisation group g on fp32 partial sums:
 //   y[m, n] = sum_g s[g, n] * ( sum_{k in g} x[m, k] (128 + q[k, n]) - (128 + z[g, n]) X[m, g] )
@@ -50,9 +50,27 @@ MOE_DEV bf16x8_v as_frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_bit_cast(bf16x8_v, v);
 }
 
-// B fragment of one packed int32 (8 k of one column): pairs (q0,q4),(q1,q5),(q2,q6),(q3,q7).
+// B fragment of one packed int32 (8 k of one column) in the k order [0,2,4,6,1,3,5,7]: the
+// nibbles are split into two byte planes (even nibbles q0 q2 q4 q6, odd nibbles q1 q3 q5 q7),
+// and each bf16 pair (128 + q_a, 128 + q_b) is one byte permute of a plane with the magic
+// exponent byte 0x43: 7 VALU operations per word.
+constexpr uint32_t kMagicBytes = 0x43434343u;
 MOE_DEV bf16x8_v weight_frag(uint32_t w) {
-  return as_frag(magic_pair(w, 0), magic_pair(w, 1), magic_pair(w, 2), magic_pair(w, 3));
+  const uint32_t ev = w & 0x0F0F0F0Fu;         // bytes q0, q2, q4, q6
+  const uint32_t od = (w >> 4) & 0x0F0F0F0Fu;  // bytes q1, q3, q5, q7
+  return as_frag(__builtin_amdgcn_perm(ev, kMagicBytes, 0x00050004u),   // (q0, q2)
+                 __builtin_amdgcn_perm(ev, kMagicBytes, 0x00070006u),   // (q4, q6)
+                 __builtin_amdgcn_perm(od, kMagicBytes, 0x00050004u),   // (q1, q3)
+                 __builtin_amdgcn_perm(od, kMagicBytes, 0x00070006u));  // (q5, q7)
+}
+
+// A fragment of 8 consecutive bf16 activations (d0 = x0|x1<<16, ..., d3 = x6|x7<<16) in the
+// k order of weight_frag: (x0,x2), (x4,x6), (x1,x3), (x5,x7).
+MOE_DEV bf16x8_v act_frag(const u32x4 d) {
+  return as_frag(__builtin_amdgcn_perm(d[1], d[0], 0x05040100u),
+                 __builtin_amdgcn_perm(d[3], d[2], 0x05040100u),
+                 __builtin_amdgcn_perm(d[1], d[0], 0x07060302u),
+                 __builtin_amdgcn_perm(d[3], d[2], 0x07060302u));
 }
 
 // Everything one lane needs for one quantisation group (SPG MFMA k-steps of 32): activations
@@ -168,9 +186,7 @@ struct DecodeTile {
     for (int t = 0; t < NT; ++t) tmp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < SPG; ++s) {
-      uint32_t xp[4];
-      xpairs(B.a[s], xp);
-      const bf16x8_v av = as_frag(xp[0], xp[1], xp[2], xp[3]);
+      const bf16x8_v av = act_frag(B.a[s]);
       tx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ones, tx, 0, 0, 0);
 #pragma unroll
       for (int p = 0; p < NP; ++p)
