@@ -36,6 +36,13 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source flags. The decode GEMMs fold each group's MFMA partial sums with VALU arithmetic:
+# MFMA results in VGPRs (instead of AGPRs) spare one v_accvgpr_read per partial sum.
+SOURCE_FLAGS = {
+    "gemm_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -49,7 +56,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
