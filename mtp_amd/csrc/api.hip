@@ -423,10 +423,11 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   // themselves (slot grid; every W1 workgroup repeats it, which costs more than the launch it
   // saves beyond two tokens); up to 8 tokens top-k and align come from one block (no align
   // launch). Beyond that the selections are spread over many workgroups: one block would
-  // serialise them on one CU.
+  // serialise them on one CU. Up to 8 tokens W2 also sums the weighted rows itself
+  // (w2_token_sum_fits).
   const bool small = topk_align_fits(T, top_k, shared ? 1 : 0);
   Routing routing = ROUTE_ALIGN;
-  if (path == MOE_PATH_DECODE && small && T <= kTokenSumMaxTokens) {
+  if (path == MOE_PATH_DECODE && small && T <= kGridTopkMaxTokens) {
     routing = ROUTE_GRID_LOGITS;
   } else if (path != MOE_PATH_PREFILL && small) {
     MOE_CHECK_HIP(launch_topk_align(logits, T, E, top_k, shared ? 1 : 0, L.bm, L.cap, ids, w,

@@ -91,9 +91,14 @@ hipError_t launch_moe_sum_bf16(const uint16_t* ys, int T, int top_k, int H, int 
                                const int32_t* ids, int num_experts, const int32_t* expert_row,
                                uint16_t* out, hipStream_t stream);
 
-// W2 and the weighted sum in one kernel for one or two tokens (decode path): block = token x
+// W2 and the weighted sum in one kernel for up to 8 tokens (decode path): block = token x
 // column tile, one wave per slot of the token, out written directly (no ys, no sum kernel).
-constexpr int kTokenSumMaxTokens = 2;
+// An expert routed by several tokens is read once per token (from L2 after the first); up to 8
+// tokens that costs less than the sum launch and the fp32 rows it saves (measured: 4 tokens
+// 27.9 -> 25.6 us per layer, 8 tokens 34.1 -> 33.4 us).
+constexpr int kTokenSumMaxTokens = 8;
+// Batches whose W1 computes the top-k itself in every workgroup (slot grid from the logits).
+constexpr int kGridTopkMaxTokens = 2;
 constexpr int kTokenSumMaxWaves = 9;  // top_k <= 8 plus the shared expert
 bool w2_token_sum_fits(const ExpertsDev& ed, const SlotsDev& sd);
 hipError_t launch_w2_token_sum(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
