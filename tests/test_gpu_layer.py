@@ -50,6 +50,14 @@ def test_small_layer(T, path):
     _check_layer(small_layer(0), T, 4, path)
 
 
+@pytest.mark.parametrize("T", [4, 8])
+def test_token_sum_w2_with_shared_expert(T):
+    """Up to 8 tokens W2 is token-major and sums each token's weighted rows itself (one wave per
+    routed slot plus one for the gated shared expert)."""
+    _say(f"token-sum W2 with shared expert T={T}")
+    _check_layer(small_layer(2, shared=True), T, 4, "decode")
+
+
 @pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode"), (16, "gemv"),
                                     (32, "decode"), (64, "decode")])
 def test_config1_full_shape(T, path):
@@ -127,11 +135,12 @@ def test_expert_row_indirection_matches_direct():
     pooled = MoeExperts(permute(layer.experts.gate), permute(layer.experts.up),
                         permute(layer.experts.down), 128,
                         expert_row=inv.to(torch.int32).cuda(), num_experts=E)
-    x = synth.make_tokens(9, 512, seed=4).cuda()
-    for path in ("decode", "prefill", "gemv"):
-        a = ops.moe_layer(x, layer.router_w, layer.experts, top_k=4, path=path)
-        b = ops.moe_layer(x, layer.router_w, pooled, top_k=4, path=path)
-        assert torch.equal(a, b)
+    for T in (6, 9):  # 6: W2 sums the token's rows itself; 9: blocked W2 + moe_sum
+        x = synth.make_tokens(T, 512, seed=4).cuda()
+        for path in ("decode", "prefill", "gemv"):
+            a = ops.moe_layer(x, layer.router_w, layer.experts, top_k=4, path=path)
+            b = ops.moe_layer(x, layer.router_w, pooled, top_k=4, path=path)
+            assert torch.equal(a, b)
 
 
 def test_workspace_reusable_across_sizes_and_paths():
