@@ -24,7 +24,7 @@
 //    and are summed through LDS in wave order (deterministic).
 //    W1 (gate_up): A = x[token(slot)], gate and up tiles, epilogue h = bf16(silu(g) * u).
 //    W2 (down):    A = h[slot], epilogue ys[slot, n] = w[slot] * y (fp32).
-//  * w2_token_sum_kernel (one or two tokens): block = one token x one column tile, wave i =
+//  * w2_token_sum_kernel (up to 8 tokens): block = one token x one column tile, wave i =
 //    the token's routed slot i (or its shared slot); the weighted rows are summed in slot order
 //    inside the block, so no separate sum kernel runs.
 // Arithmetic references: src/mtp_expert_prefetch/tracing/vllm_wna16_group_plan.py:367-486,
