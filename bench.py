@@ -51,6 +51,9 @@ def parse_args() -> argparse.Namespace:
                    help="wall-clock budget of the CPU baseline sample (0 disables it)")
     p.add_argument("--block-batches", default="1,32",
                    help="full-block batches (routed experts + gated int4 shared expert); empty disables")
+    p.add_argument("--chain-batches", default="1,64",
+                   help="decode-chain batches: the layers in a decode loop, each input the residual "
+                        "stream's RMSNorm after the previous layer (empty disables)")
     p.add_argument("--offload-tokens", type=int, default=512,
                    help="decode steps of the offloaded-expert run at batch 1 (0 disables it)")
     p.add_argument("--offload-warmup", type=int, default=16)
@@ -316,6 +319,56 @@ def main() -> int:
             del g, ws, outs
         del shared, sgate
 
+    # ------------------------------------- decode chain: the layers in a decode loop (dependent)
+    # Per layer l: y = MoE_l(h); res = res + y; h = RMSNorm_{l+1}(res) (the decoder loop around
+    # moe_forward_with_trace with mtp_rms_norm), so every layer's routing depends on the previous
+    # layer's output. Same layers, weights and routing bias as the sweep.
+    chain = {}
+    chain_batches = [int(b) for b in args.chain_batches.split(",") if b]
+    if chain_batches:
+        gn = torch.Generator().manual_seed(6000)
+        norm_w = [(0.05 * torch.randn(H, generator=gn)).to(torch.bfloat16).to(dev) for _ in range(L + 1)]
+        for T in chain_batches:
+            x0 = synth.make_tokens(T, seed=7, device=dev)
+            res = torch.empty_like(x0)
+            h = torch.empty_like(x0)
+            y = torch.empty_like(x0)
+            ws = torch.zeros(ops.workspace_bytes(T, K, layers[0].experts, False, args.decode_path),
+                             dtype=torch.uint8, device=dev)
+
+            def chain_step(record=None):
+                res.copy_(x0)
+                ops.rmsnorm(res, norm_w[0], out=h)
+                for l, ly in enumerate(layers):
+                    if record is None:
+                        ops.moe_layer(h, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
+                                      workspace=ws, out=y, path=args.decode_path)
+                    else:
+                        _, ids, _ = ops.moe_layer(h, ly.router_w, ly.experts, top_k=K,
+                                                  logit_bias=ly.logit_bias, workspace=ws, out=y,
+                                                  return_routing=True, path=args.decode_path)
+                        record.append(int(torch.unique(ids).numel()))
+                    ops.rmsnorm(res, norm_w[l + 1], add=y, out=h)
+
+            uniq = []
+            chain_step(uniq)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                chain_step()
+            for _ in range(args.warmup):
+                g.replay()
+            ts = median_event_ms(g.replay, args.steps, stream)
+            med = statistics.median(ts)
+            nbytes = sum(uniq) * per_expert
+            chain[str(T)] = {"tpot_ms_p50": med, "us_per_layer_p50": med * 1e3 / L,
+                             "us_per_layer_p95": pct(ts, 0.95) * 1e3 / L,
+                             "GBps": nbytes / (med * 1e-3) / 1e9, "U_per_layer_mean": sum(uniq) / L}
+            log(f"[bench] decode chain bs={T}: {med:.3f} ms per step ({L} layers + norms), "
+                f"{chain[str(T)]['us_per_layer_p50']:.2f} us/layer, {chain[str(T)]['GBps']:.0f} GB/s, "
+                f"U={sum(uniq) / L:.1f}")
+            del g, ws
+
     # ------------------------------------------------------------------ offloaded experts
     offload = None
     if args.offload_tokens > 0:
@@ -353,6 +406,7 @@ def main() -> int:
         "decode": {str(T): decode[T] for T in batches},
         "prefill": prefill,
         "block": block,
+        "decode_chain": chain,
         "offload": offload,
     }
     line = json.dumps(result)

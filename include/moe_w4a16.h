@@ -145,6 +145,17 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
 int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
                uint16_t* out, void* stream);
 
+/* Decoder-step norm around the MoE layer in a layer loop: when add != NULL,
+ *   res[t, :] = bf16(res[t, :] + add[t, :])   (in place, fp32 add, round to nearest even);
+ * then out[t, :] = bf16((float(res[t, :]) * rsqrt(mean(float(res[t, :])^2) + eps)) * (1 + w)).
+ * Replaces mtp_rms_norm (src/mtp_expert_prefetch/mtp/extra_tensors.py:40-48) on the residual
+ * stream of the decoder loop around moe_forward_with_trace
+ * (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:17895-17965). res, add, out: bf16
+ * [T, hidden]; weight bf16 [hidden]; hidden % 8 == 0 and <= 8192; out must not alias res.
+ * The mean is an fp32 sum in a fixed order. */
+int moe_rmsnorm_v1(uint16_t* res, const uint16_t* add, int32_t T, int32_t hidden,
+                   const uint16_t* weight, float eps, uint16_t* out, void* stream);
+
 /* Workspace bytes for moe_layer_v1 / moe_fused_experts_v1 (no state survives between calls;
  * calls that share one workspace must be ordered on one stream). */
 int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_set_v1* experts,

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_int32, c_int64, c_void_p
+from ctypes import c_float, POINTER, c_char_p, c_int32, c_int64, c_void_p
 from pathlib import Path
 
 LIB_NAME = "libmoe_w4a16.so"
@@ -40,6 +40,7 @@ EXPORTED = (
     "moe_w1_gateup_silu_v1",
     "moe_w2_down_v1",
     "moe_sum_v1",
+    "moe_rmsnorm_v1",
     "moe_layer_workspace_bytes_v1",
     "moe_layer_v1",
     "moe_fused_experts_v1",
@@ -118,6 +119,7 @@ _SIGS = {
         [_P, _I, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, _P, _I, _I, _P, _P, _I, _P],
         c_int32),
     "moe_sum_v1": ([_P, _I, _I, _I, _I, _P, _P], c_int32),
+    "moe_rmsnorm_v1": ([_P, _P, _I, _I, _P, c_float, _P, _P], c_int32),
     "moe_layer_workspace_bytes_v1": ([_I, _I, POINTER(ExpertSet), _I, _I], c_int64),
     "moe_layer_v1": (
         [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _P, _P,

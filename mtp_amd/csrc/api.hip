@@ -386,6 +386,19 @@ int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_
   return MOE_OK;
 }
 
+int moe_rmsnorm_v1(uint16_t* res, const uint16_t* add, int32_t T, int32_t hidden,
+                   const uint16_t* weight, float eps, uint16_t* out, void* stream) {
+  if (T < 0 || hidden <= 0 || hidden % 8 != 0 || hidden > 8192)
+    return fail(MOE_ERR_SHAPE, "rmsnorm: T=%d hidden=%d (hidden %% 8 == 0, <= 8192)", T, hidden);
+  if (!(eps >= 0.0f)) return fail(MOE_ERR_SHAPE, "rmsnorm: eps must be >= 0");
+  if (T == 0) return MOE_OK;
+  if (!res || !weight || !out) return fail(MOE_ERR_NULL, "rmsnorm: NULL pointer");
+  if (out == res) return fail(MOE_ERR_SHAPE, "rmsnorm: out must not alias res");
+  MOE_CHECK_HIP(launch_rmsnorm(res, add, T, hidden, weight, eps, out, (hipStream_t)stream),
+                "rmsnorm");
+  return MOE_OK;
+}
+
 int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_set_v1* experts,
                                      int32_t has_shared, int32_t path) {
   if (!experts || T < 0 || top_k < 1) return -1;

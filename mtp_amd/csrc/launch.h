@@ -127,6 +127,10 @@ hipError_t launch_predictor(const uint16_t* h, int T, int H, int L, const uint16
                             const uint16_t* w2, int E, int top_k, float* z1, uint16_t* a,
                             float* z2, int32_t* ids, float* scores, hipStream_t stream);
 
+// Residual add (add nullable) and (1 + w) RMSNorm per token row, hidden % 8 == 0, <= 8192.
+hipError_t launch_rmsnorm(uint16_t* res, const uint16_t* add, int T, int H, const uint16_t* w,
+                          float eps, uint16_t* out, hipStream_t stream);
+
 // Block sizes (slots per block) of the two paths.
 constexpr int kDecodeBlockM = 16;
 constexpr int kPrefillBlockM = 128;

@@ -205,6 +205,32 @@ def moe_sum(ys: torch.Tensor, T: int, top_k: int, has_shared: bool = False) -> t
     return out
 
 
+# ----------------------------------------------------------------------------- decoder norm
+def rmsnorm(res: torch.Tensor, weight: torch.Tensor, *, add: torch.Tensor | None = None,
+            eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Residual add (in place into ``res`` when ``add`` is given) and the (1 + w) RMSNorm of
+    mtp_rms_norm (src/mtp_expert_prefetch/mtp/extra_tensors.py:40-48) on the HIP kernel.
+
+    res, add: bf16 [T, hidden]; weight bf16 [hidden]. Returns bf16 [T, hidden]."""
+    lib = _lib.load()
+    _bf16_matrix(res, "res")
+    T, H = res.shape
+    if add is not None:
+        _bf16_matrix(add, "add", H)
+        if add.shape[0] != T:
+            raise ValueError(f"add has {add.shape[0]} rows for {T}")
+    if weight.dtype != torch.bfloat16 or weight.numel() != H or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous bfloat16 tensor of hidden elements")
+    _require_gpu(res, add, weight)
+    if out is None:
+        out = torch.empty_like(res)
+    elif out.shape != res.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor shaped like res")
+    _lib.check(lib.moe_rmsnorm_v1(res.data_ptr(), _ptr(add), T, H, weight.data_ptr(), float(eps),
+                                  out.data_ptr(), _stream()))
+    return out
+
+
 # ----------------------------------------------------------------------------- whole layer
 def workspace_bytes(T: int, top_k: int, experts: MoeExperts, has_shared: bool,
                     path: str | int = "auto") -> int:

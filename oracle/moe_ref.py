@@ -285,3 +285,21 @@ def predictor_ref(h_bits: np.ndarray, w1_bits: np.ndarray, w2_bits: np.ndarray, 
         logits.append(z2)
         ids.append(stable_topk(z2, top_k))
     return np.stack(ids), np.stack(logits)
+
+
+def rmsnorm_ref(res_bits: np.ndarray, weight_bits: np.ndarray, *, add_bits: np.ndarray | None = None,
+                eps: float = 1e-6) -> tuple[np.ndarray, np.ndarray]:
+    """Residual add and mtp_rms_norm (mtp/extra_tensors.py:40-48) in float32.
+
+    res' = bf16(res + add) (fp32 add, round to nearest even) when add is given; then
+    out = bf16((res' * rsqrt(mean(res'^2) + eps)) * (1 + w)), every step in float32 as the
+    reference's fp32 variance and (1 + weight) scaling. Returns (res' bits, out bits); the mean
+    is a float64 sum rounded to float32 (the HIP kernel sums in fp32 in its own fixed order)."""
+    x = gptq_ref.bf16_bits_to_f32(res_bits)
+    if add_bits is not None:
+        x = gptq_ref.bf16_bits_to_f32(gptq_ref.f32_to_bf16_bits((x + gptq_ref.bf16_bits_to_f32(add_bits)).astype(np.float32)))
+    var = np.float32((x.astype(np.float64) ** 2).mean(axis=-1, keepdims=True))
+    r = (np.float32(1.0) / np.sqrt(var + np.float32(eps), dtype=np.float32)).astype(np.float32)
+    w1 = (np.float32(1.0) + gptq_ref.bf16_bits_to_f32(weight_bits)).astype(np.float32)
+    out = ((x * r).astype(np.float32) * w1).astype(np.float32)
+    return gptq_ref.f32_to_bf16_bits(x), gptq_ref.f32_to_bf16_bits(out)
