@@ -253,7 +253,11 @@ MOE_DEV void decode_tile_static(const DecodeTile<NP, SPG, CT>& tile, f32x4 (&acc
   static_for<0, DEPTH - 1>([&](auto gc) { tile.load_aw(ring[gc.value], gc.value); });
   static_for<0, NGW>([&](auto gc) {
     constexpr int g = gc.value;
-    if constexpr (g + DEPTH - 1 < NGW) tile.load_aw(ring[(g + DEPTH - 1) % DEPTH], g + DEPTH - 1);
+    if constexpr (g + DEPTH - 1 < NGW) {
+      __builtin_amdgcn_s_setprio(2);  // issue the stage's loads ahead of the other waves' math
+      tile.load_aw(ring[(g + DEPTH - 1) % DEPTH], g + DEPTH - 1);
+      __builtin_amdgcn_s_setprio(0);
+    }
     __builtin_amdgcn_sched_barrier(0);  // this stage's loads before the wait for group g
     tile.compute(ring[g % DEPTH], sz[g], acc);
   });
