@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MOE_W4A16_ABI_VERSION 1
+#define MOE_W4A16_ABI_VERSION 2
 
 enum {
   MOE_OK = 0,
@@ -140,9 +140,12 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
 
 /* out[t, :] = bf16(sum_{i<top_k} ys[t*top_k + i, :] (+ ys[T*top_k + t, :])), fixed order.
  * Replaces ops.moe_sum (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19801-19804).
- * Sums every slot: moe_w2_down_v1 leaves the ys rows of dropped slots (see
- * moe_fused_experts_v1) unwritten, so a caller that may drop slots zeroes ys first. */
+ * topk_ids (device int32 [T, top_k], required) are the routed ids the W2 rows were computed
+ * for: a slot whose id is outside [0, num_experts), or whose expert has row -1 in expert_row
+ * (device int32 [num_experts], NULL = identity), is dropped and its ys row is never read
+ * (moe_w2_down_v1 does not write the rows of dropped slots). */
 int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
+               const int32_t* topk_ids, int32_t num_experts, const int32_t* expert_row,
                uint16_t* out, void* stream);
 
 /* Decoder-step norm around the MoE layer in a layer loop: when add != NULL,
@@ -237,6 +240,7 @@ typedef struct moe_slot_cache_counters_v1 {
   int64_t evicted_before_use_count;
   int64_t prefetch_bytes;
   int64_t demand_bytes;
+  int64_t prefetch_skipped_pinned_count; /* prefetches not issued: every slot was pinned */
 } moe_slot_cache_counters_v1;
 
 /* Opaque handle (a magic field is checked on every call). Not thread-safe. */
@@ -246,7 +250,13 @@ int moe_slot_cache_destroy_v1(uint64_t handle);
 /* Prefetch experts (host int32 list) of one layer on the cache's side stream (hipMemcpyAsync),
  * ordered after every kernel already enqueued on compute_stream. Replaces
  * ControlledExpertCacheManager.issue_prefetch (cache_manager.py:222-231) with real transfers.
- * issued: NULL or the number of copies started. */
+ * A prefetch never evicts a slot named by the layer's latest demand until
+ * moe_slot_cache_layer_done_v1(layer) (those slots may be read by kernels not yet enqueued);
+ * an expert for which only such slots remain is skipped. issued: NULL or the number of copies
+ * started.
+ * Call order per layer on one compute stream: demand -> enqueue the layer's kernels ->
+ * layer_done -> prefetch (for later steps). Prefetching between demand and layer_done is safe
+ * too, with the pinned slots kept out of the LRU choice. */
 int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
                                void* compute_stream, int32_t* issued);
 
@@ -256,6 +266,11 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
  * number of hits. */
 int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
                              void* compute_stream, int32_t* hits);
+
+/* The kernels that read layer's slots (after its latest demand) are enqueued: its slots may be
+ * evicted by prefetches again. Host bookkeeping only; no HIP call. No reference counterpart
+ * (the reference's cache moves no bytes, so it has no read-after-demand hazard). */
+int moe_slot_cache_layer_done_v1(uint64_t handle, int32_t layer);
 
 int moe_slot_cache_stats_v1(uint64_t handle, moe_slot_cache_counters_v1* out);
 

@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_NAME = "libmoe_w4a16.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MOE_OK = 0
 MOE_ERR_NULL = 101
@@ -50,6 +50,7 @@ EXPORTED = (
     "moe_slot_cache_destroy_v1",
     "moe_slot_cache_prefetch_v1",
     "moe_slot_cache_demand_v1",
+    "moe_slot_cache_layer_done_v1",
     "moe_slot_cache_stats_v1",
     "moe_slot_cache_slot_of_v1",
 )
@@ -74,7 +75,8 @@ class SlotCacheCounters(ctypes.Structure):
     _fields_ = [(name, c_int64) for name in (
         "capacity", "resident_count", "issued_fetch_count", "used_fetch_count",
         "unused_fetch_count", "demand_count", "demand_hit_count", "demand_miss_count",
-        "evicted_before_use_count", "prefetch_bytes", "demand_bytes")]
+        "evicted_before_use_count", "prefetch_bytes", "demand_bytes",
+        "prefetch_skipped_pinned_count")]
 
 
 class GptqProj(ctypes.Structure):
@@ -118,7 +120,7 @@ _SIGS = {
     "moe_w2_down_v1": (
         [_P, _I, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, _P, _I, _I, _P, _P, _I, _P],
         c_int32),
-    "moe_sum_v1": ([_P, _I, _I, _I, _I, _P, _P], c_int32),
+    "moe_sum_v1": ([_P, _I, _I, _I, _I, _P, _I, _P, _P, _P], c_int32),
     "moe_rmsnorm_v1": ([_P, _P, _I, _I, _P, c_float, _P, _P], c_int32),
     "moe_layer_workspace_bytes_v1": ([_I, _I, POINTER(ExpertSet), _I, _I], c_int64),
     "moe_layer_v1": (
@@ -134,6 +136,7 @@ _SIGS = {
     "moe_slot_cache_destroy_v1": ([ctypes.c_uint64], c_int32),
     "moe_slot_cache_prefetch_v1": ([ctypes.c_uint64, _I, _P, _I, _P, POINTER(c_int32)], c_int32),
     "moe_slot_cache_demand_v1": ([ctypes.c_uint64, _I, _P, _I, _P, POINTER(c_int32)], c_int32),
+    "moe_slot_cache_layer_done_v1": ([ctypes.c_uint64, _I], c_int32),
     "moe_slot_cache_stats_v1": ([ctypes.c_uint64, POINTER(SlotCacheCounters)], c_int32),
     "moe_slot_cache_slot_of_v1": ([ctypes.c_uint64, _I, _I], c_int32),
 }

@@ -243,6 +243,13 @@ int moe_predictor_v1(const uint16_t* h, int32_t T, int32_t hidden, int32_t num_h
   if (num_heads < 1 || num_heads > 1024 || (int64_t)num_heads * inner > (1 << 24))
     return fail(MOE_ERR_SHAPE, "predictor: num_heads=%d", num_heads);
   if ((int64_t)T * num_heads > (1 << 24)) return fail(MOE_ERR_SHAPE, "predictor: T * num_heads too large");
+  // The GEMV kernels address w1 ([L*D, H] bf16), w2 ([L*E, D] bf16) and h through 32-bit
+  // buffer offsets: every byte offset must stay below 2^31.
+  if ((int64_t)num_heads * inner * hidden * 2 >= (int64_t(1) << 31) ||
+      (int64_t)num_heads * num_experts * inner * 2 >= (int64_t(1) << 31) ||
+      (int64_t)T * hidden * 2 >= (int64_t(1) << 31))
+    return fail(MOE_ERR_SHAPE, "predictor: weights of %d heads (inner %d, hidden %d) exceed 2 GiB",
+                num_heads, inner, hidden);
   if (num_experts < 1 || num_experts > 512 || top_k < 1 || top_k > num_experts || top_k > 64)
     return fail(MOE_ERR_SHAPE, "predictor: num_experts=%d top_k=%d", num_experts, top_k);
   if (workspace_bytes < moe_predictor_workspace_bytes_v1(T, num_heads, inner, num_experts, top_k))
@@ -375,13 +382,15 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
 }
 
 int moe_sum_v1(const float* ys, int32_t T, int32_t top_k, int32_t hidden, int32_t has_shared,
+               const int32_t* topk_ids, int32_t num_experts, const int32_t* expert_row,
                uint16_t* out, void* stream) {
-  if (T < 0 || top_k < 1 || hidden <= 0 || hidden % 4 != 0)
-    return fail(MOE_ERR_SHAPE, "moe_sum: T=%d top_k=%d hidden=%d", T, top_k, hidden);
+  if (T < 0 || top_k < 1 || hidden <= 0 || hidden % 4 != 0 || num_experts < 1)
+    return fail(MOE_ERR_SHAPE, "moe_sum: T=%d top_k=%d hidden=%d num_experts=%d", T, top_k,
+                hidden, num_experts);
   if (T == 0) return MOE_OK;
-  if (!ys || !out) return fail(MOE_ERR_NULL, "moe_sum: NULL pointer");
-  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, hidden, has_shared ? 1 : 0, nullptr, 0, nullptr, out,
-                               (hipStream_t)stream),
+  if (!ys || !out || !topk_ids) return fail(MOE_ERR_NULL, "moe_sum: NULL pointer");
+  MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, hidden, has_shared ? 1 : 0, topk_ids, num_experts,
+                               expert_row, out, (hipStream_t)stream),
                 "moe_sum");
   return MOE_OK;
 }

@@ -8,14 +8,18 @@
 // miss inserts the key as used; evicting a prefetched-but-unused entry counts as
 // evicted-before-use. Unlike the reference (accounting only), the bytes really move.
 //
-// Ordering:
-//  * a prefetch first makes the side stream wait for all work enqueued so far on the compute
-//    stream, so a slot is never overwritten while a kernel may still read it;
+// Ordering (one compute stream per handle):
 //  * a demand makes the compute stream wait for the layer's pending prefetches, fetches its
 //    misses on the compute stream, and uploads the layer's expert->slot table (from a pinned
-//    staging ring) on the compute stream before the layer's kernels.
-// The table entry of an absent expert points at slot 0 (kernels only read rows of routed,
-// demanded experts). Handles are not thread-safe: one handle per host thread.
+//    staging ring) on the compute stream before the layer's kernels;
+//  * the slots a demand names are pinned: a prefetch never picks them as victims until
+//    moe_slot_cache_layer_done_v1 says the layer's kernels are enqueued (or the layer's next
+//    demand, whose copies are ordered after those kernels on the compute stream, replaces the
+//    pins). A prefetch that finds only pinned slots skips that expert;
+//  * a prefetch first makes the side stream wait for all work enqueued so far on the compute
+//    stream, so an unpinned slot is never overwritten while an enqueued kernel may read it.
+// The table entry of an absent expert is -1: the kernels drop the slots routed to it (they
+// contribute zero). Handles are not thread-safe: one handle per host thread.
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -36,6 +40,7 @@ struct Slot {
   int expert = -1;
   bool prefetched = false;
   bool used = false;
+  bool pinned = false;  // named by the layer's latest demand; its kernels may not be enqueued yet
   uint64_t last_use = 0;
 };
 
@@ -98,13 +103,20 @@ char* device_slot(const Cache* c, int layer, int slot) {
 // expert that a later entry of the same demand list names; that entry then misses and is
 // fetched again. With at most slots_per_layer distinct experts per call, every expert of the
 // list is resident when the call returns (the last touches of the call are its experts).
-int pick_slot(const Layer& L) {
+// A prefetch passes skip_pinned: it never takes a slot the latest demand named (-1 if every
+// slot is pinned).
+int pick_slot(const Layer& L, bool skip_pinned) {
   int best = -1;
   for (int s = 0; s < (int)L.slots.size(); ++s) {
+    if (skip_pinned && L.slots[s].pinned) continue;
     if (L.slots[s].expert < 0) return s;
     if (best < 0 || L.slots[s].last_use < L.slots[best].last_use) best = s;
   }
   return best;
+}
+
+void unpin(Layer& L) {
+  for (Slot& sl : L.slots) sl.pinned = false;
 }
 
 void evict(Cache* c, Layer& L, int s) {
@@ -188,14 +200,19 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
       L.slots[L.slot_of[e]].last_use = ++c->tick;
       continue;
     }
-    c->st.issued_fetch_count++;
     if (c->d.slots_per_layer == 0) {  // nothing can be kept: counts as evicted before use
+      c->st.issued_fetch_count++;
       c->st.evicted_before_use_count++;
       continue;
     }
-    const int s = pick_slot(L);
+    const int s = pick_slot(L, true);
+    if (s < 0) {  // every slot holds an expert the layer's enqueued-or-pending kernels read
+      c->st.prefetch_skipped_pinned_count++;
+      continue;
+    }
+    c->st.issued_fetch_count++;
     evict(c, L, s);
-    L.slots[s] = Slot{e, true, false, ++c->tick};
+    L.slots[s] = Slot{e, true, false, false, ++c->tick};
     L.slot_of[e] = s;
     ++count;
     if (live(c)) {
@@ -238,6 +255,9 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
       return fail(MOE_ERR_SHAPE, "slot cache demand: more distinct experts than slots");
   }
   hipStream_t cs = (hipStream_t)compute_stream;
+  // The previous demand's kernels were enqueued on the compute stream before this call, so
+  // its pins can go: this demand's copies and the prefetches after it are ordered after them.
+  unpin(L);
   if (L.pending && live(c)) {
     SC_HIP(hipStreamWaitEvent(cs, L.prefetch_done, 0), "compute waits prefetch");
     L.pending = false;
@@ -253,14 +273,17 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
       Slot& sl = L.slots[s];
       if (sl.prefetched && !sl.used) c->st.used_fetch_count++;
       sl.used = true;
+      sl.pinned = true;
       sl.last_use = ++c->tick;
       continue;
     }
     c->st.demand_miss_count++;
     if (c->d.slots_per_layer == 0) continue;
-    s = pick_slot(L);
+    // With at most slots_per_layer distinct experts per call, the LRU victim is never an expert
+    // this call already touched (those hold the newest ticks).
+    s = pick_slot(L, false);
     evict(c, L, s);
-    L.slots[s] = Slot{e, false, true, ++c->tick};
+    L.slots[s] = Slot{e, false, true, true, ++c->tick};
     L.slot_of[e] = s;
     if (live(c)) {
       SC_HIP(hipMemcpyAsync(device_slot(c, layer, s), host_blob(c, layer, e), c->d.expert_bytes,
@@ -280,6 +303,15 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
     SC_HIP(hipEventRecord(c->staging_done[r], cs), "record staging");
   }
   if (hits) *hits = nh;
+  return MOE_OK;
+}
+
+int moe_slot_cache_layer_done_v1(uint64_t handle, int32_t layer) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  if (layer < 0 || layer >= c->d.num_layers)
+    return fail(MOE_ERR_SHAPE, "slot cache layer_done: bad layer");
+  unpin(c->layers[layer]);
   return MOE_OK;
 }
 

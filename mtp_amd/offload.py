@@ -162,6 +162,11 @@ class SlotCache:
                                                       self._stream(stream), ctypes.byref(hits)))
         return hits.value
 
+    def layer_done(self, layer: int) -> None:
+        """The kernels reading the layer's slots (after its latest demand) are enqueued: its
+        slots may be taken by prefetches again."""
+        _lib.check(self._lib.moe_slot_cache_layer_done_v1(self.handle, layer))
+
     def stats(self) -> dict[str, int]:
         c = _lib.SlotCacheCounters()
         _lib.check(self._lib.moe_slot_cache_stats_v1(self.handle, ctypes.byref(c)))
@@ -265,6 +270,9 @@ class OffloadedExperts:
     def demand(self, layer: int, experts, stream=None) -> int:
         return self.cache.demand(layer, experts, stream)
 
+    def layer_done(self, layer: int) -> None:
+        self.cache.layer_done(layer)
+
     def stats(self) -> dict[str, int]:
         return self.cache.stats()
 
@@ -292,6 +300,7 @@ def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts
     torch.cuda.current_stream().synchronize()
     pool.demand(layer, ids_host.reshape(-1).tolist())
     out = ops.fused_experts(x, ids, w, pool.layer_experts(layer), path=path, workspace=workspace)
+    pool.layer_done(layer)
     return out, ids_host
 
 

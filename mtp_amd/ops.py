@@ -183,11 +183,17 @@ def w1_gateup_silu(x, experts: MoeExperts, sorted_ids, expert_ids, ntpp, *, top_
 
 
 def w2_down(h, experts: MoeExperts, sorted_ids, expert_ids, ntpp, topk_weights_flat, *, T: int,
-            top_k: int, shared: MoeExperts | None = None, path: str | int = "auto") -> torch.Tensor:
+            top_k: int, shared: MoeExperts | None = None, path: str | int = "auto",
+            ys: torch.Tensor | None = None) -> torch.Tensor:
+    """Weighted W2 rows ys fp32 [slots, H]; rows of dropped slots are left as they were."""
     lib = _lib.load()
     p = _path(path)
     bm = _block_m(p, T, top_k)
-    ys = torch.empty(h.shape[0], experts.hidden_size, dtype=torch.float32, device=h.device)
+    if ys is None:
+        ys = torch.empty(h.shape[0], experts.hidden_size, dtype=torch.float32, device=h.device)
+    elif (ys.dtype != torch.float32 or tuple(ys.shape) != (h.shape[0], experts.hidden_size)
+          or not ys.is_contiguous()):
+        raise ValueError("ys must be contiguous float32 [slots, hidden]")
     ex = experts.struct()
     sh = shared.struct() if shared is not None else None
     _lib.check(lib.moe_w2_down_v1(
@@ -197,11 +203,23 @@ def w2_down(h, experts: MoeExperts, sorted_ids, expert_ids, ntpp, topk_weights_f
     return ys
 
 
-def moe_sum(ys: torch.Tensor, T: int, top_k: int, has_shared: bool = False) -> torch.Tensor:
+def moe_sum(ys: torch.Tensor, topk_ids: torch.Tensor, experts: MoeExperts,
+            has_shared: bool = False) -> torch.Tensor:
+    """Fixed-order fp32 sum of each token's weighted W2 rows -> bf16 [T, H]. Slots whose id is
+    outside [0, E) or whose expert is not resident in a slot pool are skipped (w2_down leaves
+    their rows unwritten)."""
     lib = _lib.load()
+    if topk_ids.dtype != torch.int32 or topk_ids.ndim != 2:
+        raise TypeError("topk_ids must be int32 [T, k]")
+    _require_gpu(ys, topk_ids)
+    T, top_k = topk_ids.shape
     H = ys.shape[1]
+    if ys.dtype != torch.float32 or ys.shape[0] < T * top_k + (T if has_shared else 0):
+        raise ValueError("ys must be float32 [T*k (+T), H]")
     out = torch.empty(T, H, dtype=torch.bfloat16, device=ys.device)
-    _lib.check(lib.moe_sum_v1(ys.data_ptr(), T, top_k, H, int(has_shared), out.data_ptr(), _stream()))
+    _lib.check(lib.moe_sum_v1(ys.data_ptr(), T, top_k, H, int(has_shared), topk_ids.data_ptr(),
+                              int(experts.num_experts), _ptr(experts.expert_row), out.data_ptr(),
+                              _stream()))
     return out
 
 

@@ -12,9 +12,14 @@ the fused HIP kernels instead of being dequantised to dense bf16 at load time.
   load_repacked_projection_tensors / dequantize_repacked_projection :151-184
   apply_dequantized_projection :187-188
   load_single_expert_weights   :191-228 (dense dequantised weights, via the HIP kernel)
-  SingleExpertMlp              :231-256 (int4 expert, fused W1/W2 kernels)
-  TopKExpertMlp                :259-327 (int4 experts, fused W1/W2 kernels)
-  load_single_expert_mlp / load_topk_expert_mlp :330-371
+  SingleExpertMlp              :231-256 (int4 expert as non-persistent buffers, fused W1/W2
+                                         kernels; gate_proj/up_proj/down_proj dequantised on use)
+  TopKExpertMlp                :259-327 (int4 experts stacked as buffers, fused W1/W2 kernels)
+  load_single_expert_mlp / load_topk_expert_mlp :330-371 (bf16, fp16 and fp32 dtypes)
+
+Activations enter the kernels as bf16: an fp16 or fp32 input is rounded to bf16, the expert sum
+is accumulated in fp32 and returned in the input's dtype. Dense SingleExpertWeights have no int4
+form and are refused with a TypeError.
 """
 
 from __future__ import annotations
@@ -174,10 +179,15 @@ def dequantize_gptq_projection(
                f"num_groups={num_groups}")
         raise ValueError(msg)
     group_size = rows_in // num_groups
-    return ops.dequantize(tensors.qweight.contiguous(), tensors.qzeros.contiguous(),
-                          tensors.scales.to(torch.float16).contiguous(),
-                          tensors.g_idx.to(torch.int32).contiguous(), group_size=group_size,
-                          linear_weight=linear_weight, dtype=target_dtype)
+    # The dequant runs on the HIP kernel. Host tensors are staged to the current ROCm device
+    # and the result is returned on their device, as the reference returns it on the input's.
+    home = tensors.qweight.device
+    dev = home if home.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
+    out = ops.dequantize(tensors.qweight.to(dev).contiguous(), tensors.qzeros.to(dev).contiguous(),
+                         tensors.scales.to(device=dev, dtype=torch.float16).contiguous(),
+                         tensors.g_idx.to(device=dev, dtype=torch.int32).contiguous(),
+                         group_size=group_size, linear_weight=linear_weight, dtype=target_dtype)
+    return out if home.type == "cuda" else out.to(home)
 
 
 def synthesize_g_idx(qweight: torch.Tensor, *, bits: int = 4, group_size: int = 128) -> torch.Tensor:
@@ -228,62 +238,166 @@ def load_single_expert_weights(store: RepackedMoeExpertStore, *, layer: int, exp
     return weights
 
 
-def _stack(experts: list[QuantizedExpertWeights], attr: str) -> GptqStack:
-    ps = [getattr(e, attr) for e in experts]
-    return GptqStack(torch.stack([p.qweight for p in ps]).contiguous(),
-                     torch.stack([p.qzeros for p in ps]).contiguous(),
-                     torch.stack([p.scales.to(torch.float16) for p in ps]).contiguous(),
-                     torch.stack([p.g_idx.to(torch.int32) for p in ps]).contiguous())
-
-
 def _as_quantized(weights) -> QuantizedExpertWeights:
     if isinstance(weights, QuantizedExpertWeights):
         return weights
-    raise TypeError(
-        "the W4A16 expert kernels take int4 GPTQ tensors (QuantizedExpertWeights); dense "
-        "SingleExpertWeights have no int4 form to run")
+    if isinstance(weights, SingleExpertWeights):
+        raise TypeError(
+            "SingleExpertMlp runs int4 GPTQ experts on the W4A16 kernels and takes "
+            "QuantizedExpertWeights (load_single_expert_mlp / load_quantized_expert); dense "
+            "SingleExpertWeights have no int4 form to run")
+    raise TypeError(f"expected QuantizedExpertWeights, got {type(weights).__name__}")
 
 
-class SingleExpertMlp(torch.nn.Module):
-    """y = W_down (silu(W_gate x) * (W_up x)) on int4 weights (gptq_unpack.py:231-256)."""
+_KINDS = ("qweight", "qzeros", "scales")
 
-    def __init__(self, weights: QuantizedExpertWeights) -> None:
-        super().__init__()
-        q = _as_quantized(weights)
-        self.quantized = q
-        self.stack = MoeExperts(_stack([q], "gate_proj"), _stack([q], "up_proj"),
-                                _stack([q], "down_proj"), q.group_size)
-        self.stack.validate()
+
+class _Int4ExpertStack(torch.nn.Module):
+    """int4 GPTQ stacks of n experts held as non-persistent buffers
+    ``{proj}_{kind}`` ([n, ...]), so ``parameters()/buffers()``, ``.to()`` and ``.cuda()`` see
+    and move them as they see the reference modules' dense weight buffers. The MoeExperts view
+    the kernels take is rebuilt from the buffers after every move."""
+
+    def _init_stack(self, experts: list[QuantizedExpertWeights], dtype) -> None:
+        self.compute_dtype = resolve_torch_dtype(dtype)
+        if self.compute_dtype not in ops.OUT_DTYPES:
+            raise ValueError(f"Unsupported dtype {self.compute_dtype}")
+        group = experts[0].group_size
+        stacks = {}
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            ps = [getattr(e, proj) for e in experts]
+            st = GptqStack(torch.stack([p.qweight for p in ps]).contiguous(),
+                           torch.stack([p.qzeros for p in ps]).contiguous(),
+                           torch.stack([p.scales.to(torch.float16) for p in ps]).contiguous(),
+                           torch.stack([p.g_idx.to(torch.int32) for p in ps]).contiguous())
+            stacks[proj] = st
+        # shapes, dtypes and g_idx[k] == k // group are checked once, here
+        MoeExperts(stacks["gate_proj"], stacks["up_proj"], stacks["down_proj"], group).validate()
+        for proj, st in stacks.items():
+            for kind in _KINDS:
+                self.register_buffer(f"{proj}_{kind}", getattr(st, kind), persistent=False)
+        self.group_size = int(group)
+        self._view: MoeExperts | None = None
+        self._dense: dict = {}
+
+    def _apply(self, fn, recurse=True):
+        out = super()._apply(fn, recurse)
+        self._view = None
+        self._dense = {}
+        return out
+
+    def _stack_of(self, proj: str) -> GptqStack:
+        return GptqStack(*(getattr(self, f"{proj}_{kind}") for kind in _KINDS))
+
+    def int4_experts(self) -> MoeExperts:
+        """The stacks as the kernels' MoeExperts (validated at construction)."""
+        if self._view is None:
+            view = MoeExperts(self._stack_of("gate_proj"), self._stack_of("up_proj"),
+                              self._stack_of("down_proj"), self.group_size)
+            view._validated = True
+            self._view = view
+        return self._view
+
+    def _dequantized(self, proj: str, row: int = 0) -> torch.Tensor:
+        """Dense Linear-orientation weight of one projection of stack row ``row`` in the
+        module's dtype, dequantised bit-exactly by the HIP kernel on first use."""
+        key = (proj, row)
+        if key not in self._dense:
+            st = self._stack_of(proj)
+            self._dense[key] = ops.dequantize(st.qweight[row], st.qzeros[row], st.scales[row],
+                                              group_size=self.group_size, linear_weight=True,
+                                              dtype=self.compute_dtype)
+        return self._dense[key]
 
     @property
     def hidden_size(self) -> int:
-        return self.stack.hidden_size
+        return int(self.gate_proj_qweight.shape[1]) * 8
 
     @property
     def intermediate_size(self) -> int:
-        return self.stack.intermediate_size
+        return int(self.gate_proj_qweight.shape[2])
 
-    def forward(self, input_tensor: torch.Tensor) -> torch.Tensor:
+    def _run(self, input_tensor: torch.Tensor, rows: list[int], weights: torch.Tensor | None):
+        """out[t] = sum_i w_i * expert_{rows[i]}(x[t]) on the fused kernels. Activations enter
+        the kernels as bf16 (fp16/fp32 inputs are rounded to bf16); the sum is accumulated in
+        fp32 and returned in the input's dtype."""
         if input_tensor.shape[-1] != self.hidden_size:
             msg = f"Expected input last dim {self.hidden_size}, got {input_tensor.shape[-1]}"
             raise ValueError(msg)
-        x = input_tensor.reshape(-1, self.hidden_size).contiguous()
-        T = x.shape[0]
-        ids = torch.zeros(T, 1, dtype=torch.int32, device=x.device)
-        w = torch.ones(T, 1, dtype=torch.float32, device=x.device)
-        out = ops.fused_experts(x, ids, w, self.stack)
-        return out.reshape(input_tensor.shape)
+        if input_tensor.dtype not in ops.OUT_DTYPES:
+            raise TypeError(f"input dtype {input_tensor.dtype} is not one of bf16/fp16/fp32")
+        experts = self.int4_experts()
+        if input_tensor.device != experts.device:
+            msg = (f"input on {input_tensor.device}, expert weights on {experts.device}; the "
+                   "W4A16 kernels run on a ROCm device (move the module with .to('cuda'))")
+            raise ValueError(msg)
+        x = input_tensor.reshape(-1, self.hidden_size).to(torch.bfloat16).contiguous()
+        T, k = x.shape[0], len(rows)
+        dev = x.device
+        ids = torch.tensor(rows, dtype=torch.int32, device=dev).expand(T, k).contiguous()
+        if weights is None:
+            w = torch.ones(T, k, dtype=torch.float32, device=dev)
+        else:
+            w = weights.to(torch.float32).expand(T, k).contiguous()
+        out = ops.fused_experts(x, ids, w, experts)
+        return out.to(input_tensor.dtype).reshape(input_tensor.shape)
 
 
-class TopKExpertMlp(torch.nn.Module):
-    """sum_i w_i * expert_{id_i}(x) over one shared expert set (gptq_unpack.py:259-327)."""
+class SingleExpertMlp(_Int4ExpertStack):
+    """y = W_down (silu(W_gate x) * (W_up x)) on int4 weights (gptq_unpack.py:231-256).
 
-    def __init__(self, experts: dict[int, SingleExpertMlp | QuantizedExpertWeights]) -> None:
+    ``gate_proj`` / ``up_proj`` / ``down_proj`` are the dense Linear-orientation weights the
+    reference module holds, dequantised bit-exactly on first access in ``dtype``; the forward
+    reads the int4 buffers, never the dense copies."""
+
+    def __init__(self, weights: QuantizedExpertWeights, *,
+                 dtype: str | torch.dtype = torch.bfloat16) -> None:
+        super().__init__()
+        q = _as_quantized(weights)
+        self._init_stack([q], dtype)
+
+    @property
+    def gate_proj(self) -> torch.Tensor:
+        return self._dequantized("gate_proj")
+
+    @property
+    def up_proj(self) -> torch.Tensor:
+        return self._dequantized("up_proj")
+
+    @property
+    def down_proj(self) -> torch.Tensor:
+        return self._dequantized("down_proj")
+
+    def quantized(self) -> QuantizedExpertWeights:
+        """The expert's int4 tensors (views of this module's buffers)."""
+        projs = {}
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            st = self._stack_of(proj)
+            g = torch.arange(st.in_features, dtype=torch.int32, device=st.qweight.device)
+            projs[proj] = GptqProjectionTensors(st.qweight[0], st.qzeros[0], st.scales[0],
+                                                g // self.group_size)
+        return QuantizedExpertWeights(projs["gate_proj"], projs["up_proj"], projs["down_proj"],
+                                      self.group_size)
+
+    def forward(self, input_tensor: torch.Tensor) -> torch.Tensor:
+        return self._run(input_tensor, [0], None)
+
+
+class TopKExpertMlp(_Int4ExpertStack):
+    """sum_i w_i * expert_{id_i}(x) over one shared expert set (gptq_unpack.py:259-327).
+
+    The loaded experts are stacked in ascending id order into one int4 stack (buffers
+    ``{proj}_{kind}`` [n, ...]); ``experts`` maps str(id) to a SingleExpertMlp over that
+    expert's rows, as the reference's ModuleDict does."""
+
+    def __init__(self, experts: dict[int, SingleExpertMlp | QuantizedExpertWeights], *,
+                 dtype: str | torch.dtype | None = None) -> None:
         super().__init__()
         if not experts:
             msg = "TopKExpertMlp requires at least one expert"
             raise ValueError(msg)
-        quant = {int(k): (v.quantized if isinstance(v, SingleExpertMlp) else _as_quantized(v))
+        dtypes = {v.compute_dtype for v in experts.values() if isinstance(v, SingleExpertMlp)}
+        quant = {int(k): (v.quantized() if isinstance(v, SingleExpertMlp) else _as_quantized(v))
                  for k, v in experts.items()}
         hidden_sizes = {q.hidden_size for q in quant.values()}
         intermediate_sizes = {q.intermediate_size for q in quant.values()}
@@ -291,11 +405,10 @@ class TopKExpertMlp(torch.nn.Module):
             msg = (f"All experts must share dimensions; got hidden={hidden_sizes}, "
                    f"intermediate={intermediate_sizes}")
             raise ValueError(msg)
+        if dtype is None:
+            dtype = dtypes.pop() if len(dtypes) == 1 else torch.bfloat16
         self._ids = tuple(sorted(quant))
-        ordered = [quant[i] for i in self._ids]
-        self.stack = MoeExperts(_stack(ordered, "gate_proj"), _stack(ordered, "up_proj"),
-                                _stack(ordered, "down_proj"), ordered[0].group_size)
-        self.stack.validate()
+        self._init_stack([quant[i] for i in self._ids], dtype)
         self._row = {eid: row for row, eid in enumerate(self._ids)}
 
     @property
@@ -303,12 +416,19 @@ class TopKExpertMlp(torch.nn.Module):
         return self._ids
 
     @property
-    def hidden_size(self) -> int:
-        return self.stack.hidden_size
-
-    @property
-    def intermediate_size(self) -> int:
-        return self.stack.intermediate_size
+    def experts(self) -> dict[str, SingleExpertMlp]:
+        out = {}
+        for eid, row in self._row.items():
+            projs = {}
+            for proj in ("gate_proj", "up_proj", "down_proj"):
+                st = self._stack_of(proj)
+                g = torch.arange(st.in_features, dtype=torch.int32, device=st.qweight.device)
+                projs[proj] = GptqProjectionTensors(st.qweight[row], st.qzeros[row],
+                                                    st.scales[row], g // self.group_size)
+            out[str(eid)] = SingleExpertMlp(
+                QuantizedExpertWeights(projs["gate_proj"], projs["up_proj"], projs["down_proj"],
+                                       self.group_size), dtype=self.compute_dtype)
+        return out
 
     def forward(self, input_tensor: torch.Tensor, expert_ids: torch.Tensor,
                 expert_weights: torch.Tensor) -> torch.Tensor:
@@ -331,15 +451,9 @@ class TopKExpertMlp(torch.nn.Module):
                 msg = f"Expert {expert_id} is not loaded; loaded={self.loaded_expert_ids}"
                 raise KeyError(msg)
             rows.append(self._row[int(expert_id)])
-        x = input_tensor.reshape(-1, self.hidden_size).contiguous()
-        T, k = x.shape[0], len(rows)
-        dev = x.device
-        ids = torch.tensor(rows, dtype=torch.int32, device=dev).expand(T, k).contiguous()
-        # the reference casts the routing weights to the input dtype before use (:319)
-        w = expert_weights.to(device=dev, dtype=input_tensor.dtype).to(torch.float32)
-        w = w.expand(T, k).contiguous()
-        out = ops.fused_experts(x, ids, w, self.stack)
-        return out.reshape(input_tensor.shape)
+        # the reference casts the routing weights to the input's device and dtype (:319)
+        w = expert_weights.to(device=input_tensor.device, dtype=input_tensor.dtype)
+        return self._run(input_tensor, rows, w)
 
 
 def load_quantized_expert(store: RepackedMoeExpertStore, *, layer: int, expert: int,
@@ -351,30 +465,29 @@ def load_quantized_expert(store: RepackedMoeExpertStore, *, layer: int, expert: 
     return QuantizedExpertWeights(projs["gate_proj"], projs["up_proj"], projs["down_proj"], group)
 
 
-def _check_bits_dtype(bits: int, dtype) -> None:
+def _check_bits(bits: int) -> None:
     _validate_bits(bits)
     if bits != 4:
         raise NotImplementedError("the fused expert kernels implement 4-bit GPTQ")
-    if resolve_torch_dtype(dtype) != torch.bfloat16:
-        raise NotImplementedError("the fused expert kernels compute with bf16 activations")
 
 
 def load_single_expert_mlp(store: RepackedMoeExpertStore, *, layer: int, expert: int,
                            bits: int = 4, dtype: str | torch.dtype = torch.bfloat16,
                            device: str | torch.device = "cuda") -> SingleExpertMlp:
-    _check_bits_dtype(bits, dtype)
-    return SingleExpertMlp(load_quantized_expert(store, layer=layer, expert=expert, device=device))
+    _check_bits(bits)
+    return SingleExpertMlp(load_quantized_expert(store, layer=layer, expert=expert, device=device),
+                           dtype=dtype)
 
 
 def load_topk_expert_mlp(store: RepackedMoeExpertStore, *, layer: int,
                          expert_ids: list[int] | tuple[int, ...], bits: int = 4,
                          dtype: str | torch.dtype = torch.bfloat16,
                          device: str | torch.device = "cuda") -> TopKExpertMlp:
-    _check_bits_dtype(bits, dtype)
+    _check_bits(bits)
     unique_expert_ids = tuple(dict.fromkeys(int(expert_id) for expert_id in expert_ids))
     experts = {eid: load_quantized_expert(store, layer=layer, expert=eid, device=device)
                for eid in unique_expert_ids}
-    return TopKExpertMlp(experts)
+    return TopKExpertMlp(experts, dtype=dtype)
 
 
 def _validate_single_expert_weights(weights: SingleExpertWeights) -> None:

@@ -12,7 +12,6 @@ are made on the CPU (device-independent bytes) and copied.
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
@@ -142,4 +141,3 @@ def prefill_flops(T: int, top_k: int = TOP_K, hidden: int = HIDDEN,
 
 assert expert_bytes() == 1_634_304
 assert prefill_flops(2048) == 103_079_215_104
-_ = math  # keep the import for the calibration helper

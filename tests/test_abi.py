@@ -76,3 +76,23 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("MTP_AMD_LIB", str(tmp_path / "absent.so"))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.load()
+
+
+def test_predictor_rejects_weights_beyond_32_bit_offsets():
+    """The predictor's GEMV kernels use 32-bit buffer offsets: heads whose bf16 weights reach
+    2 GiB are refused before any launch (here 40 heads of 8192 x 4096 = 2.5 GiB of w1)."""
+    lib = _lib.load()
+    ws_need = lib.moe_predictor_workspace_bytes_v1(1, 40, 8192, 256, 16)
+    rc = lib.moe_predictor_v1(0x10, 1, 4096, 40, 0x10, 8192, 0x10, 256, 16, 0x10, ws_need, 0x10,
+                              None)
+    assert rc == _lib.MOE_ERR_SHAPE
+    assert b"exceed 2 GiB" in lib.moe_w4a16_last_error()
+    # the full-size workload shape (40 heads of 1024 x 2048) is accepted by the checks
+    ws_need = lib.moe_predictor_workspace_bytes_v1(1, 40, 1024, 256, 16)
+    assert ws_need > 0
+
+
+def test_moe_sum_requires_the_routed_ids():
+    lib = _lib.load()
+    rc = lib.moe_sum_v1(0x10, 4, 8, 2048, 0, None, 256, None, 0x10, None)
+    assert rc == _lib.MOE_ERR_NULL

@@ -80,3 +80,99 @@ def test_single_expert_mlp(store_dir):
     assert moe_ref.rel_err(out.float().cpu().numpy(), ref) <= LAYER_RTOL
     with pytest.raises(ValueError):
         mlp(torch.zeros(2, H + 8, dtype=torch.bfloat16, device="cuda"))
+
+
+@pytest.mark.parametrize("dtype_name", ["bf16", "fp16", "fp32"])
+def test_topk_harness_call_sequence(store_dir, dtype_name):
+    """The call sequence of the reference's top-k smoke harness
+    (scripts/smoke_topk_expert_mlp.py:65-119): resolve the dtype name, open the store as a
+    context manager, load the deduplicated experts, find the device through
+    next(parameters(), next(buffers())), draw [batch, seq, hidden] inputs in that dtype, call
+    the module under inference_mode with CPU long ids and device weights of the same dtype,
+    then read the reported fields. The output is checked against the oracle."""
+    from mtp_amd.repack import resolve_torch_dtype
+    d, ex = store_dir
+    target = resolve_torch_dtype(dtype_name)
+    expert_ids = [4, 0, 7, 4]
+    expert_weights = [0.4, 0.3, 0.2, 0.1]
+    torch.manual_seed(0)
+    with RepackedMoeExpertStore(d) as store:
+        mlp = load_topk_expert_mlp(store, layer=0, expert_ids=expert_ids, bits=4, dtype=target,
+                                   device="cuda")
+    device = next(mlp.parameters(), next(mlp.buffers())).device
+    assert device.type == "cuda"
+    x = torch.randn(2, 3, mlp.hidden_size, device=device, dtype=target)
+    ids = torch.tensor(expert_ids, dtype=torch.long)
+    weights = torch.tensor(expert_weights, dtype=target, device=device)
+    with torch.inference_mode():
+        out = mlp(x, ids, weights)
+    assert bool(torch.isfinite(out).all().item())
+    assert list(mlp.loaded_expert_ids) == [0, 4, 7]
+    assert out.shape == x.shape and out.dtype == target
+    assert (mlp.hidden_size, mlp.intermediate_size) == (H, I)
+    # oracle: the kernels take bf16 activations, so the oracle input is the input rounded to
+    # bf16; the routing weights are the harness's weights in its dtype
+    xb = x.reshape(6, H).to(torch.bfloat16)
+    w_np = np.tile(weights.float().cpu().numpy(), (6, 1))
+    ref = moe_ref.moe_layer_f32(bf16_bits(xb), np.tile(np.array(expert_ids, np.int32), (6, 1)),
+                                w_np, experts_to_np(ex))
+    err = moe_ref.rel_err(out.reshape(6, H).float().cpu().numpy(), ref)
+    print(f"  {dtype_name}: rel_err={err:.3e}", flush=True)
+    assert err <= LAYER_RTOL
+    # the same module moved to the CPU and back runs again from its buffers
+    mlp.to("cpu")
+    assert next(mlp.buffers()).device.type == "cpu"
+    with pytest.raises(ValueError):
+        mlp(x.cpu(), ids, weights.cpu())
+    mlp.to(device)
+    with torch.inference_mode():
+        again = mlp(x, ids, weights)
+    assert torch.equal(again, out)
+
+
+@pytest.mark.parametrize("dtype_name", ["bf16", "fp16", "fp32"])
+def test_single_expert_harness_call_sequence(store_dir, dtype_name):
+    """The call sequence of the reference's single-expert smoke harness
+    (scripts/smoke_single_expert_mlp.py:43-87): load one expert, draw inputs on
+    mlp.gate_proj.device in mlp.gate_proj.dtype, run it, and report the projection shapes.
+    gate_proj / up_proj / down_proj are the bit-exact dequantised weights."""
+    from mtp_amd.repack import resolve_torch_dtype
+    d, ex = store_dir
+    target = resolve_torch_dtype(dtype_name)
+    torch.manual_seed(0)
+    with RepackedMoeExpertStore(d) as store:
+        mlp = load_single_expert_mlp(store, layer=0, expert=2, bits=4, dtype=target, device="cuda")
+    x = torch.randn(2, 4, mlp.hidden_size, device=mlp.gate_proj.device, dtype=mlp.gate_proj.dtype)
+    with torch.inference_mode():
+        out = mlp(x)
+    assert bool(torch.isfinite(out).all().item())
+    assert str(mlp.gate_proj.dtype).replace("torch.", "") == str(target).replace("torch.", "")
+    assert list(mlp.gate_proj.shape) == [I, H] and list(mlp.up_proj.shape) == [I, H]
+    assert list(mlp.down_proj.shape) == [H, I]
+    assert out.shape == x.shape and out.dtype == target
+    for proj, st in (("gate_proj", ex.gate), ("up_proj", ex.up), ("down_proj", ex.down)):
+        want = gptq_ref.dequant_f32(st.qweight[2].numpy(), st.qzeros[2].numpy(), f16_bits(st.scales[2]))
+        got = getattr(mlp, proj).float().cpu().numpy()
+        # (q - z) * s is exact in fp32; the module's dtype rounds it once (RNE)
+        want_t = torch.from_numpy(want).to(target).float().numpy()
+        assert np.array_equal(got, want_t), proj
+    xb = x.reshape(8, H).to(torch.bfloat16)
+    ref = moe_ref.moe_layer_f32(bf16_bits(xb), np.full((8, 1), 2, np.int32),
+                                np.ones((8, 1), np.float32), experts_to_np(ex))
+    err = moe_ref.rel_err(out.reshape(8, H).float().cpu().numpy(), ref)
+    print(f"  {dtype_name}: rel_err={err:.3e}", flush=True)
+    assert err <= LAYER_RTOL
+
+
+def test_dequantize_host_tensors_on_the_gpu(store_dir):
+    """dequantize_gptq_projection given host tensors dequantises on the ROCm device and returns
+    the result on the host, bit-exact."""
+    from mtp_amd.repack import load_repacked_projection_tensors, dequantize_gptq_projection
+    d, ex = store_dir
+    with RepackedMoeExpertStore(d) as store:
+        t = load_repacked_projection_tensors(store, layer=0, expert=1, projection="gate_proj")
+    out = dequantize_gptq_projection(t, dtype="fp16", linear_weight=False)
+    assert out.device.type == "cpu" and out.dtype == torch.float16 and out.shape == (H, I)
+    want = gptq_ref.dequant_f32(ex.gate.qweight[1].numpy(), ex.gate.qzeros[1].numpy(),
+                                f16_bits(ex.gate.scales[1]), linear_weight=False)
+    assert np.array_equal(out.numpy(), want.astype(np.float16))

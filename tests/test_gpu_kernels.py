@@ -127,3 +127,32 @@ def test_align_known_answer():
     assert int(n.item()) == 12
     assert e.cpu().tolist()[:3] == [1, 2, 3]
     assert s.cpu().tolist()[:12] == [0, 3, 3, 3, 1, 3, 3, 3, 2, 3, 3, 3]
+
+
+@pytest.mark.parametrize("path", ["decode", "prefill", "gemv"])
+def test_stepwise_entry_points_with_dropped_ids_and_poisoned_ys(path):
+    """align -> W1 -> W2 -> moe_sum as separate entry points, with ids outside [0, E) and a ys
+    buffer full of NaN: moe_sum skips the dropped slots' rows (W2 never writes them)."""
+    from mtp_amd import synth
+    from tests.helpers import LAYER_RTOL, experts_to_np, small_layer, to_gpu
+    lay = small_layer(6)
+    g = to_gpu(lay)
+    T, k, E = 12, 4, 16
+    rng = np.random.default_rng(60)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    drop = rng.random(ids.shape) < 0.25
+    ids[drop] = rng.choice([-3, E, E + 7], size=int(drop.sum()))
+    w = rng.uniform(0.1, 0.6, ids.shape).astype(np.float32)
+    x = synth.make_tokens(T, 512, seed=61)
+    xd, idd, wd = x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    bm = ops.PREFILL_BLOCK_M if path == "prefill" else ops.DECODE_BLOCK_M
+    sorted_ids, eids, ntpp = ops.align(idd, E, bm)
+    h = ops.w1_gateup_silu(xd, g.experts, sorted_ids, eids, ntpp, top_k=k, path=path)
+    ys = torch.full((T * k, 512), float("nan"), dtype=torch.float32, device="cuda")
+    ops.w2_down(h, g.experts, sorted_ids, eids, ntpp, wd.reshape(-1), T=T, top_k=k, path=path, ys=ys)
+    out = ops.moe_sum(ys, idd, g.experts)
+    torch.cuda.synchronize()
+    ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(lay.experts))
+    err = moe_ref.rel_err(out.float().cpu().numpy(), ref)
+    print(f"  {path}: rel_err={err:.3e}", flush=True)
+    assert np.isfinite(err) and err <= LAYER_RTOL

@@ -272,3 +272,53 @@ def test_fused_prefill_align_layout(shared):
     want = sorted(range(nblk), key=lambda b: (-cls[b], b))
     got_border = i32[o["border"] // 4: o["border"] // 4 + nblk]
     assert list(got_border) == want
+
+
+@pytest.mark.parametrize("T", [8, 64])
+def test_config2_zipf_decode_full_shape(T):
+    """Config 2 at full shape with the Zipf(1.1) routing skew, decode path, against the oracle
+    (ids bit-exact, weights, layer output)."""
+    _say(f"config2 zipf decode T={T}")
+    _check_layer(synth.make_layer(T % 40, zipf=True), T, 8, "decode", seed=100 + T)
+
+
+def _hottest_last_block_tokens(ids: np.ndarray, block_m: int) -> tuple[int, np.ndarray]:
+    """Tokens of the hottest expert's last align block (slots sorted by flat id within the
+    expert's group, so the last block holds its highest flat ids)."""
+    flat = ids.reshape(-1)
+    counts = np.bincount(flat, minlength=int(flat.max()) + 1)
+    hot = int(np.argmax(counts))
+    slots = np.nonzero(flat == hot)[0]
+    c = len(slots)
+    start = (-(-c // block_m) - 1) * block_m
+    return hot, np.unique(slots[start:] // ids.shape[1])
+
+
+def test_config3_prefill_full_shape_zipf():
+    """Config 3: 2048 tokens through one full-shape layer with Zipf(1.1) skew on the prefill
+    path. Every token's ids are compared bit-exact; the output is compared against the oracle
+    on a token subsample that holds every token of the hottest expert's last align block, a
+    stride-16 sample and the last token."""
+    T, k = 2048, 8
+    _say(f"config3 prefill T={T}")
+    layer_cpu = synth.make_layer(3, zipf=True)
+    g = to_gpu(layer_cpu)
+    x = synth.make_tokens(T, seed=7)
+    out, ids, w = ops.moe_layer(x.cuda(), g.router_w, g.experts, top_k=k,
+                                logit_bias=g.logit_bias, path="prefill", return_routing=True)
+    torch.cuda.synchronize()
+    x_bits = bf16_bits(x)
+    r_ids, r_w, _ = moe_ref.router_topk(x_bits, bf16_bits(layer_cpu.router_w), k,
+                                        layer_cpu.logit_bias.numpy())
+    assert np.array_equal(ids.cpu().numpy(), r_ids), "routing ids must be bit-exact"
+    np.testing.assert_allclose(w.cpu().numpy(), r_w, rtol=2e-6, atol=1e-7)
+    counts = np.bincount(r_ids.reshape(-1), minlength=256)
+    hot, hot_tokens = _hottest_last_block_tokens(r_ids, ops.PREFILL_BLOCK_M)
+    _say(f"  hottest expert {hot}: {counts[hot]} slots "
+         f"({-(-counts[hot] // ops.PREFILL_BLOCK_M)} blocks), last block {len(hot_tokens)} tokens")
+    assert counts[hot] > 8 * ops.PREFILL_BLOCK_M  # the skew spreads the expert over many blocks
+    sub = np.unique(np.concatenate([hot_tokens, np.arange(0, T, 16), [T - 1]]))
+    ref = moe_ref.moe_layer_f32(x_bits[sub], r_ids[sub], r_w[sub], experts_to_np(layer_cpu.experts))
+    err = moe_ref.rel_err(out.float().cpu().numpy()[sub], ref)
+    _say(f"  {len(sub)} tokens checked, rel_err={err:.3e}")
+    assert err <= LAYER_RTOL

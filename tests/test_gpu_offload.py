@@ -145,3 +145,26 @@ def test_nonresident_expert_is_dropped(pooled, path):
     err = moe_ref.rel_err(got.float().cpu().numpy(), ref)
     _say(f"  rel_err={err:.3e}")
     assert np.isfinite(err) and err <= LAYER_RTOL
+
+
+def test_prefetch_between_demand_and_kernels_keeps_demanded_slots(pooled):
+    """demand -> prefetch -> kernels on one stream: the prefetch may not take a slot the demand
+    published (the kernels that read it are enqueued after the prefetch's copies start), so the
+    output equals the resident layer's and the demanded slots keep their experts."""
+    layers, pool = pooled
+    layer = 0
+    g = layers[layer]
+    x = synth.make_tokens(2, 512, seed=91).cuda()
+    ids, w, _, _ = ops.router_topk(x, g.router_w, 4, logit_bias=g.logit_bias)
+    demanded = sorted(set(ids.cpu().reshape(-1).tolist()))
+    pool.demand(layer, demanded)
+    slots = {e: pool.cache.slot_of(layer, e) for e in demanded}
+    others = [e for e in range(16) if e not in demanded]
+    pool.prefetch(layer, others)  # more experts than free slots: LRU pressure on every slot
+    assert {e: pool.cache.slot_of(layer, e) for e in demanded} == slots
+    got = ops.fused_experts(x, ids, w, pool.layer_experts(layer), path="decode")
+    pool.layer_done(layer)
+    want = ops.fused_experts(x, ids, w, g.experts, path="decode")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    _slot_bytes_ok(pool, layer, demanded, pack_blobs(g.experts))

@@ -56,6 +56,7 @@ def test_reference_lru_cases():
         assert c.prefetch(0, [1]) == 0 and not o[0].issue_prefetch(0, 1)  # resident: no issue
         assert c.demand(0, [1]) == 1 and o[0].demand(0, 1)                 # used prefetch
         assert c.demand(0, [2]) == 0 and not o[0].demand(0, 2)             # miss inserts
+        c.layer_done(0)                                                     # kernels enqueued
         c.prefetch(0, [3]); o[0].issue_prefetch(0, 3)                       # evicts 1 (LRU)
         c.prefetch(0, [4]); o[0].issue_prefetch(0, 4)                       # evicts 2
         c.prefetch(0, [5]); o[0].issue_prefetch(0, 5)                       # evicts 3 unused
@@ -91,9 +92,36 @@ def test_random_sequences_match_oracle(layers, experts, slots, seed):
             else:
                 hits = c.demand(layer, ids)
                 assert hits == sum(oracles[layer].demand(layer, e) for e in ids)
+                c.layer_done(layer)  # the layer's kernels are enqueued
             if step % 50 == 0:
                 _check(c, oracles)
         _check(c, oracles)
+
+
+def test_prefetch_never_evicts_slots_of_the_latest_demand():
+    """Between a demand and layer_done the demanded slots may still be read by kernels that are
+    not enqueued yet: a prefetch takes other slots, or skips when only pinned slots remain."""
+    _lib_or_skip()
+    with SlotCache(1, 16, 3, 16, dry_run=True) as c:
+        c.demand(0, [1, 2])
+        s1, s2 = c.slot_of(0, 1), c.slot_of(0, 2)
+        assert c.prefetch(0, [5]) == 1          # the free slot
+        assert c.prefetch(0, [6]) == 1          # evicts 5 (the only unpinned), not 1 or 2
+        assert c.slot_of(0, 5) == -1 and c.slot_of(0, 6) >= 0
+        assert (c.slot_of(0, 1), c.slot_of(0, 2)) == (s1, s2)
+        c.demand(0, [1, 2, 6])                  # every slot pinned
+        assert c.prefetch(0, [7]) == 0
+        st = c.stats()
+        assert st["prefetch_skipped_pinned_count"] == 1 and c.slot_of(0, 7) == -1
+        assert st["evicted_before_use_count"] == 1          # 5 was evicted unused
+        c.layer_done(0)
+        assert c.prefetch(0, [7]) == 1          # LRU again: evicts 1
+        assert c.slot_of(0, 1) == -1 and c.slot_of(0, 7) >= 0
+        # the next demand of the layer replaces the pins of the previous one
+        c.demand(0, [2])
+        assert c.prefetch(0, [8]) == 1 and c.slot_of(0, 2) >= 0
+        with pytest.raises(_lib.MoeLibraryError):
+            c.layer_done(1)
 
 
 def test_bad_arguments_raise():
