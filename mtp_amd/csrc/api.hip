@@ -116,7 +116,7 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Workspace of moe_layer_v1 / moe_fused_experts_v1 (no state survives between calls).
 struct Workspace {
-  size_t logits, ids, w, sorted, eids, ntpp, border, h, ys, total;
+  size_t logits, norms, ids, w, sorted, eids, ntpp, border, h, ys, total;
   int cap, bm;
 };
 
@@ -128,6 +128,7 @@ Workspace layout(int T, int top_k, const moe_expert_set_v1* ex, int has_shared, 
   L.cap = align_capacity_blocks(T, top_k, E, has_shared, L.bm);
   size_t o = 0;
   L.logits = o; o += align256((size_t)T * (E + 1) * 4);
+  L.norms = o;  o += align256((size_t)(E + 1) * 4);  // router-row norms of the prefill router
   L.ids = o;    o += align256((size_t)T * top_k * 4);
   L.w = o;      o += align256(slots * 4);
   L.sorted = o; o += align256((size_t)L.cap * L.bm * 4);
@@ -212,6 +213,19 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   MOE_CHECK_HIP(launch_moe_sum(ys, T, top_k, ex->hidden, has_shared, ids, ex->num_experts,
                                ex->expert_row, out, stream),
                 "moe_sum");
+  return MOE_OK;
+}
+
+// The layer's routing for a caller that asked for it (ids_out / weights_out nullable).
+int copy_routing(const int32_t* ids, const float* w, int T, int top_k, int32_t* ids_out,
+                 float* weights_out, hipStream_t s) {
+  if (ids_out)
+    MOE_CHECK_HIP(hipMemcpyAsync(ids_out, ids, (size_t)T * top_k * 4, hipMemcpyDeviceToDevice, s),
+                  "copy ids");
+  if (weights_out)
+    MOE_CHECK_HIP(hipMemcpyAsync(weights_out, w, (size_t)T * top_k * 4, hipMemcpyDeviceToDevice,
+                                 s),
+                  "copy weights");
   return MOE_OK;
 }
 
@@ -438,6 +452,16 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   float* logits = at<float>(workspace, L.logits);
   int32_t* ids = at<int32_t>(workspace, L.ids);
   float* w = at<float>(workspace, L.w);
+  if (path == MOE_PATH_PREFILL && router_prefill_fits(T, experts->hidden, E, top_k)) {
+    // approximate MFMA logits, certified top-k with canonical logits for the selection
+    MOE_CHECK_HIP(launch_router_prefill(x, T, experts->hidden, router_w, E,
+                                        shared ? shared_gate_w : nullptr, logit_bias, top_k,
+                                        logits, at<float>(workspace, L.norms), ids, w, s),
+                  "router (prefill)");
+    rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, ROUTE_ALIGN, s);
+    if (rc) return rc;
+    return copy_routing(ids, w, T, top_k, topk_ids_out, topk_weights_out, s);
+  }
   MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E,
                                      shared ? shared_gate_w : nullptr, logit_bias, logits, s),
                 "router logits");
@@ -463,13 +487,7 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   }
   rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, routing, s);
   if (rc) return rc;
-  if (topk_ids_out)
-    MOE_CHECK_HIP(hipMemcpyAsync(topk_ids_out, ids, (size_t)T * top_k * 4,
-                                 hipMemcpyDeviceToDevice, s), "copy ids");
-  if (topk_weights_out)
-    MOE_CHECK_HIP(hipMemcpyAsync(topk_weights_out, w, (size_t)T * top_k * 4,
-                                 hipMemcpyDeviceToDevice, s), "copy weights");
-  return MOE_OK;
+  return copy_routing(ids, w, T, top_k, topk_ids_out, topk_weights_out, s);
 }
 
 int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,

@@ -20,6 +20,16 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
                                 hipStream_t stream);
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
                               int32_t* ids, float* weights, hipStream_t stream);
+// Prefill-size router (router_mfma.hip): approximate logits on MFMA into approx [T][E+1] and
+// squared router-row norms into nw2 [E], then per token a certified top-k whose ids, order and
+// weights equal those of the canonical logits (weights[T*top_k + t] = shared gate when
+// shared_w is given). H % 512 == 0, H <= 2048, E <= 512.
+bool router_prefill_fits(int T, int H, int E, int top_k);
+float router_prefill_rel_bound(int H);
+hipError_t launch_router_prefill(const uint16_t* x, int T, int H, const uint16_t* W, int E,
+                                 const uint16_t* shared_w, const float* bias, int top_k,
+                                 float* approx, float* nw2, int32_t* ids, float* weights,
+                                 hipStream_t stream);
 // Top-k of every token (one wave each) and the align/sort of the at most 64 slots by one wave,
 // in one launch: the decode-size routing tail. sorted/eids are written up to the padded total
 // only (the decode kernels read nothing past it); ntpp holds the total.

@@ -137,24 +137,15 @@ MOE_DEV uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// One wave: the top_k (<= 64) largest of row[0..E) (E <= 64 * MAXC), larger logit first and
-// equal logits by lower id (the reference's tie rule made explicit). Lane r < top_k receives
-// the r-th selection (id, logit). Every logit is loaded at once (lanes past E read zeros
-// without a memory access and are masked out). A round is a 32-bit wave maximum plus one ballot
-// per column to find the lowest id holding it; the value comes back from the key.
+// One wave: the top_k (<= 64) largest keys, larger key first and equal keys by lower id (the
+// reference's tie rule made explicit). key[c] of lane l belongs to id l + 64 c; key 0 marks
+// "not a candidate" (there must be at least top_k candidates). A round is a 32-bit wave
+// maximum plus one ballot per column to find the lowest id holding it; the selected keys are
+// cleared to 0. Lane r < top_k receives the r-th selection (id, key).
 template <int MAXC>
-MOE_DEV void topk_select(const float* __restrict__ row, int E, int top_k, int lane, int& my_i,
-                         float& my_v) {
-  const __amdgpu_buffer_rsrc_t rr = buf_rsrc(row, (uint32_t)E * 4u);
-  float v[MAXC];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) v[c] = __uint_as_float(buf_ld32(rr, (uint32_t)(lane + 64 * c) * 4u));
-  uint32_t key[MAXC];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c)  // masked with an AND: a select of a loaded value would become
-                                  // a branch around the load with a wait inside it
-    key[c] = topk_ord(v[c]) & (0u - (uint32_t)(lane + 64 * c < E));
-  my_v = 0.0f;
+MOE_DEV void topk_select_keys(uint32_t (&key)[MAXC], int top_k, int lane, int& my_i,
+                              uint32_t& my_key) {
+  my_key = 0u;
   my_i = 0;
   for (int r = 0; r < top_k; ++r) {
     uint32_t m = key[0];
@@ -172,9 +163,29 @@ MOE_DEV void topk_select(const float* __restrict__ row, int E, int top_k, int la
       if (lane + 64 * c == sel) key[c] = 0u;
     if (lane == r) {
       my_i = sel;
-      my_v = topk_ord_value(m);
+      my_key = m;
     }
   }
+}
+
+// One wave: the top_k (<= 64) largest of row[0..E) (E <= 64 * MAXC), larger logit first and
+// equal logits by lower id. Lane r < top_k receives the r-th selection (id, logit). Every logit
+// is loaded at once (lanes past E read zeros without a memory access and are masked out).
+template <int MAXC>
+MOE_DEV void topk_select(const float* __restrict__ row, int E, int top_k, int lane, int& my_i,
+                         float& my_v) {
+  const __amdgpu_buffer_rsrc_t rr = buf_rsrc(row, (uint32_t)E * 4u);
+  float v[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) v[c] = __uint_as_float(buf_ld32(rr, (uint32_t)(lane + 64 * c) * 4u));
+  uint32_t key[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c)  // masked with an AND: a select of a loaded value would become
+                                  // a branch around the load with a wait inside it
+    key[c] = topk_ord(v[c]) & (0u - (uint32_t)(lane + 64 * c < E));
+  uint32_t my_key;
+  topk_select_keys<MAXC>(key, top_k, lane, my_i, my_key);
+  my_v = (lane < top_k) ? topk_ord_value(my_key) : 0.0f;
 }
 
 // Renormalised weight of lane r's selection: exp(l_r - l_0) / sum_{j < k} exp(l_j - l_0).

@@ -223,12 +223,12 @@ def test_decode_repeated_ids(case):
 
 def _workspace_offsets(T, k, E, has_shared, bm, cap):
     """Byte offsets of the routing sections of a layer workspace, in the library's order
-    (logits, ids, weights, sorted slot ids, block experts, ntpp, block order; each 256-byte
-    aligned)."""
+    (logits, router-row norms, ids, weights, sorted slot ids, block experts, ntpp, block order;
+    each 256-byte aligned)."""
     def a256(n):
         return (n + 255) // 256 * 256
     slots = T * k + (T if has_shared else 0)
-    sizes = (("logits", T * (E + 1) * 4), ("ids", T * k * 4), ("w", slots * 4),
+    sizes = (("logits", T * (E + 1) * 4), ("norms", (E + 1) * 4), ("ids", T * k * 4), ("w", slots * 4),
              ("sorted", cap * bm * 4), ("eids", cap * 4), ("ntpp", 256), ("border", cap * 4))
     off, out = 0, {}
     for name, n in sizes:
@@ -322,3 +322,41 @@ def test_config3_prefill_full_shape_zipf():
     err = moe_ref.rel_err(out.float().cpu().numpy()[sub], ref)
     _say(f"  {len(sub)} tokens checked, rel_err={err:.3e}")
     assert err <= LAYER_RTOL
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_prefill_router_certificate_on_ties(shared):
+    """The prefill router selects on approximate MFMA logits and recomputes canonical logits for
+    the candidates its error bound cannot separate. Router rows that are exactly equal (ties:
+    the lower id first) or one bf16 ulp apart (near-ties inside the bound) force that path; ids
+    and weights must still equal the oracle's canonical ones for every token."""
+    T, k, E, H = 384, 8, 64, 1024
+    _say(f"prefill router certificate on ties T={T} shared={shared}")
+    layer = synth.make_layer(7, num_experts=E, hidden=H, intermediate=256, shared=shared)
+    rw = layer.router_w.float().clone()
+    g = torch.Generator().manual_seed(77)
+    v = torch.randn(H, generator=g) * 0.05
+    for e in (3, 9, 10, 40):          # exact ties
+        rw[e] = v
+    near = v.to(torch.bfloat16).float().clone()
+    near[17] = torch.nextafter(near[17].to(torch.bfloat16), torch.tensor(1e9).to(torch.bfloat16)).float()
+    rw[11] = near                      # one ulp away in one element
+    rw[41] = -v                        # the opposite direction: never selected with the others
+    layer.router_w = rw.to(torch.bfloat16)
+    gl = to_gpu(layer)
+    x = synth.make_tokens(T, H, seed=78)
+    out, ids, w = ops.moe_layer(x.cuda(), gl.router_w, gl.experts, top_k=k, shared=gl.shared,
+                                shared_gate_w=gl.shared_gate_w, path="prefill",
+                                return_routing=True)
+    torch.cuda.synchronize()
+    r_ids, r_w, r_logits = moe_ref.router_topk(bf16_bits(x), bf16_bits(layer.router_w), k)
+    tied = np.isin(r_ids, [3, 9, 10, 11, 40]).sum(axis=1)
+    _say(f"  tokens with >= 2 tied experts in the top-{k}: {int((tied >= 2).sum())}")
+    assert (tied >= 2).sum() > T // 4
+    assert np.array_equal(ids.cpu().numpy(), r_ids), "routing ids must be bit-exact"
+    np.testing.assert_allclose(w.cpu().numpy(), r_w, rtol=2e-6, atol=1e-7)
+    if shared:
+        sg = moe_ref.shared_gate(bf16_bits(x), bf16_bits(layer.shared_gate_w))
+        ref = moe_ref.moe_layer_f32(bf16_bits(x), r_ids, r_w, experts_to_np(layer.experts),
+                                    shared=experts_to_np(layer.shared), shared_gate_values=sg)
+        assert moe_ref.rel_err(out.float().cpu().numpy(), ref) <= LAYER_RTOL
