@@ -175,6 +175,21 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
                  uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
                  void* stream);
 
+/* moe_layer_v1 without a workspace argument and without any allocation: the workspace is a
+ * file-scope device array of moe_layer_noalloc_max_bytes_v1() bytes (64 MiB) per GPU, held until
+ * the process ends. No counterpart in the reference: for callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * Returns MOE_ERR_WORKSPACE when the call needs more than that (moe_layer_workspace_bytes_v1;
+ * at hidden 2048, 256 experts, intermediate 512, top-8: above about 890 tokens). Calls
+ * on one GPU share its array: calls that overlap on one GPU (several streams or host threads)
+ * race; calls ordered on one stream do not. */
+int64_t moe_layer_noalloc_max_bytes_v1(void);
+int moe_layer_noalloc_v1(const uint16_t* x, int32_t T, const uint16_t* router_w,
+                         const float* logit_bias, int32_t top_k, const moe_expert_set_v1* experts,
+                         const moe_expert_set_v1* shared, const uint16_t* shared_gate_w,
+                         uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out,
+                         int32_t path, void* stream);
+
 /* Experts with caller-given routing: topk_ids int32 [T, top_k], topk_weights fp32 [T, top_k].
  * Replaces TopKExpertMlp.forward (src/mtp_expert_prefetch/repack/gptq_unpack.py:293-327)
  * and moe_tokens with given ids (src/mtp_expert_prefetch/mtp/extra_tensors.py:544-598).

@@ -44,6 +44,8 @@ EXPORTED = (
     "moe_layer_workspace_bytes_v1",
     "moe_layer_v1",
     "moe_fused_experts_v1",
+    "moe_layer_noalloc_max_bytes_v1",
+    "moe_layer_noalloc_v1",
     "moe_predictor_workspace_bytes_v1",
     "moe_predictor_v1",
     "moe_slot_cache_create_v1",
@@ -126,6 +128,10 @@ _SIGS = {
     "moe_layer_v1": (
         [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _P, _P,
          _I, _P],
+        c_int32),
+    "moe_layer_noalloc_max_bytes_v1": ([], c_int64),
+    "moe_layer_noalloc_v1": (
+        [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, _P, _P, _I, _P],
         c_int32),
     "moe_fused_experts_v1": (
         [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _I, _P],
