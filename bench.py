@@ -47,7 +47,7 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--prefill-tokens", type=int, default=2048)
     p.add_argument("--decode-path", default="decode", choices=["decode", "gemv"],
                    help="decode GEMM kernels: MFMA with in-register dequant, or VALU dot2 GEMV")
-    p.add_argument("--cpu-baseline-seconds", type=float, default=20.0,
+    p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="wall-clock budget of the CPU baseline sample (0 disables it)")
     p.add_argument("--block-batches", default="1,32",
                    help="full-block batches (routed experts + gated int4 shared expert); empty disables")
@@ -249,6 +249,64 @@ def main() -> int:
     roofline["frac"] = roofline["achieved"] / roofline["peak"]
     log(f"[bench] W1 decode bs={Tr}: {w1_launch_us:.2f} us/launch, {roofline['achieved']:.0f} GB/s")
 
+    # ------------------------------- W1 / W2 latency buckets (the reference's measurement unit)
+    # W1 = gate_up of 1 token x top-8, W2 = down of those 8 rows with top_k = 1, each launch
+    # bracketed by its own HIP events (eager, not captured), as the reference's GPU-event
+    # latencies of the wna16 kernels (vllm_router_trace.py:14321-14326, reduced to p50/p95/p99
+    # by summarize_wna16_w1w2_timing.py:13-28).
+    buckets = {}
+    if True:
+        xb = synth.make_tokens(1, seed=7, device=dev)
+        hb = torch.empty(K, I, dtype=torch.bfloat16, device=dev)
+        yb = torch.empty(K, H, dtype=torch.float32, device=dev)
+        routed1 = []
+        for ly in layers:
+            ids1, w1_, _, _ = ops.router_topk(xb, ly.router_w, K, logit_bias=ly.logit_bias)
+            s1, e1, n1 = ops.align(ids1, E, ops.DECODE_BLOCK_M)
+            routed1.append((s1, e1, n1, w1_.reshape(-1).contiguous()))
+        st1 = ctypes.c_void_p(stream.cuda_stream)
+
+        def w1_launch(ex, r):
+            _lib.check(lib.moe_w1_gateup_silu_v1(xb.data_ptr(), 1, K, ctypes.byref(ex), None,
+                                                 r[0].data_ptr(), r[1].data_ptr(), r[2].data_ptr(),
+                                                 ops.DECODE_BLOCK_M, r[1].numel(), hb.data_ptr(),
+                                                 ops.PATHS["decode"], st1))
+
+        def w2_launch(ex, r):
+            _lib.check(lib.moe_w2_down_v1(hb.data_ptr(), 1, K, ctypes.byref(ex), None,
+                                          r[0].data_ptr(), r[1].data_ptr(), r[2].data_ptr(),
+                                          ops.DECODE_BLOCK_M, r[1].numel(), r[3].data_ptr(),
+                                          yb.data_ptr(), ops.PATHS["decode"], st1))
+        samples = {"w1": [], "w2": []}
+        for rep in range(args.warmup + max(args.steps // 2, 5)):
+            evs = []
+            for ex, r in zip(structs, routed1):
+                for name, fn in (("w1", w1_launch), ("w2", w2_launch)):
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    fn(ex, r)
+                    b.record(stream)
+                    evs.append((name, a, b))
+            torch.cuda.synchronize()
+            if rep >= args.warmup:
+                for name, a, b in evs:
+                    samples[name].append(a.elapsed_time(b) * 1e3)
+        for name, xs in samples.items():
+            buckets[name + "_us"] = {"p50": pct(xs, 0.5), "p95": pct(xs, 0.95), "p99": pct(xs, 0.99),
+                                     "samples": len(xs)}
+        buckets["workload"] = (f"batch 1 over the {L} Zipf layers: W1 = gate_up + SiLU*mul of 1 token "
+                               f"x top-{K} (moe_w1_gateup_silu_v1), W2 = down of those {K} rows with "
+                               "top_k = 1 and the routed weight (moe_w2_down_v1); one HIP event pair "
+                               "per eager launch")
+        buckets["reference_w7900"] = {"w1_us": {"p50": 135.05, "p95": 148.63},
+                                      "w2_us": {"p50": 79.71, "p95": 96.45},
+                                      "source": "PROGRESS.md:19498-19509 (vLLM Triton wna16, AWQ, "
+                                                "Radeon PRO W7900)"}
+        log(f"[bench] W1/W2 buckets bs=1: W1 p50 {buckets['w1_us']['p50']:.2f} us "
+            f"p95 {buckets['w1_us']['p95']:.2f}; W2 p50 {buckets['w2_us']['p50']:.2f} us "
+            f"p95 {buckets['w2_us']['p95']:.2f}")
+
     # ------------------------------------------------------------------ prefill-2048
     Tp = args.prefill_tokens
     prefill = {}
@@ -379,7 +437,8 @@ def main() -> int:
     # ------------------------------------------------------------------ CPU baseline
     cpu = None
     if args.cpu_baseline_seconds > 0:
-        cpu = cpu_baseline(layers, batches, args.cpu_baseline_seconds, per_expert)
+        cpu = cpu_baseline(layers, batches, args.cpu_baseline_seconds, per_expert,
+                           Tp if Tp > 0 else 0, block_batches)
 
     result = {
         "metric": METRIC,
@@ -404,6 +463,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "decode": {str(T): decode[T] for T in batches},
+        "decode_buckets": buckets,
         "prefill": prefill,
         "block": block,
         "decode_chain": chain,
@@ -506,71 +566,147 @@ def offload_bench(layers, args, dev) -> dict:
     }
 
 
-def cpu_baseline(layers, batches, budget_s: float, per_expert: int) -> dict:
-    """The oracle's reference-faithful CPU path (dequantise at load, bf16 F.linear per expert,
-    the moe_tokens slot loop, fp32 router) timed on the host cores over a bounded sample:
-    layers 0..3 at every decode batch, median of 3 repetitions each."""
+CPU_REPS = 5
+
+
+def _cpu_threads() -> tuple[int, int]:
+    """(threads used, cores in this process's affinity set). The harness of a shared GPU box sets
+    OMP_NUM_THREADS to the box's CPU share; the baseline then uses that share, else every core of
+    the affinity set."""
+    affinity = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    threads = min(affinity, int(share)) if share and share.isdigit() and int(share) > 0 else affinity
+    return threads, affinity
+
+
+def _cpu_layer(ly, torch):
+    return (ly.router_w.cpu(), ly.logit_bias.cpu() if ly.logit_bias is not None else None,
+            {n: (st.qweight.cpu(), st.qzeros.cpu(), st.scales.cpu())
+             for n, st in (("gate", ly.experts.gate), ("up", ly.experts.up), ("down", ly.experts.down))})
+
+
+def _cpu_dequant(stacks, used, moe_ref, torch):
+    sel = torch.tensor(used)
+    deq = {n: torch.cat([moe_ref.dequant_stack_torch(q[c], z[c], s[c]) for c in sel.split(32)])
+           for n, (q, z, s) in stacks.items()}
+    return {e: (deq["gate"][i], deq["up"][i], deq["down"][i]) for i, e in enumerate(used)}
+
+
+def _cpu_route(x, router, bias, F, torch):
+    lg = F.linear(x, router).float()
+    if bias is not None:
+        lg = lg + bias
+    p = torch.softmax(lg, dim=-1)
+    w, ids = torch.topk(p, 8, dim=-1)
+    return ids, w / w.sum(-1, keepdim=True).clamp_min(1e-20)
+
+
+def cpu_baseline(layers, batches, budget_s: float, per_expert: int, prefill_tokens: int,
+                 block_batches: list[int]) -> dict:
+    """The oracle's reference-faithful CPU path timed on the host cores (not the optimisation
+    target): dequantise at load (gptq_unpack.py:88-131), then per call the fp32 router
+    (softmax -> top-8 -> renormalise) and the moe_tokens slot loop of bf16 F.linear per routed
+    expert (extra_tensors.py:544-598). Median of CPU_REPS repetitions per case.
+      * decode: layers 0..3 at every decode batch (a bounded sample of the 40-layer sweep; the
+        GB/s figure uses the same algorithmic expert bytes as the GPU metric);
+      * prefill: the full prefill batch through layer 0 (TFLOP/s on the same useful FLOPs);
+      * full block: the decode block batches through layer 0 with a gated int4 shared expert.
+    The dequant-inclusive variant adds the dequantisation of the routed experts to each call."""
     import torch
     import torch.nn.functional as F
 
     from mtp_amd import synth
     from oracle import moe_ref
 
-    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
-    torch.set_num_threads(cores)
+    threads, affinity = _cpu_threads()
+    torch.set_num_threads(threads)
     t_start = time.time()
+
+    def timed(fn):
+        reps = []
+        for _ in range(CPU_REPS):
+            t1 = time.perf_counter()
+            fn()
+            reps.append(time.perf_counter() - t1)
+        return statistics.median(reps)
+
     sample_layers = min(4, len(layers))
     tot_bytes = tot_s = tot_s_deq = 0.0
     done = []
     for l in range(sample_layers):
-        ly = layers[l]
-        router = ly.router_w.cpu()
-        bias = ly.logit_bias.cpu()
-        stacks = {n: (st.qweight.cpu(), st.qzeros.cpu(), st.scales.cpu())
-                  for n, st in (("gate", ly.experts.gate), ("up", ly.experts.up), ("down", ly.experts.down))}
+        router, bias, stacks = _cpu_layer(layers[l], torch)
         for T in batches:
             if time.time() - t_start > budget_s:
                 break
             x = synth.make_tokens(T, seed=7).to(torch.bfloat16)
-            logits = F.linear(x, router).float() + bias
-            p = torch.softmax(logits, dim=-1)
-            w, ids = torch.topk(p, 8, dim=-1)
-            w = w / w.sum(-1, keepdim=True).clamp_min(1e-20)
+            ids, _ = _cpu_route(x, router, bias, F, torch)
             used = torch.unique(ids).tolist()
-            sel = torch.tensor(used)
             t_deq = time.perf_counter()
-            deq = {n: torch.cat([moe_ref.dequant_stack_torch(q[c], z[c], s[c]) for c in sel.split(32)])
-                   for n, (q, z, s) in stacks.items()}
+            experts = _cpu_dequant(stacks, used, moe_ref, torch)
             t_deq = time.perf_counter() - t_deq
-            experts = {e: (deq["gate"][i], deq["up"][i], deq["down"][i]) for i, e in enumerate(used)}
-            reps = []
-            for _ in range(3):
-                t1 = time.perf_counter()
-                lg = F.linear(x, router).float() + bias
-                pp = torch.softmax(lg, dim=-1)
-                ww, ii = torch.topk(pp, 8, dim=-1)
-                ww = ww / ww.sum(-1, keepdim=True).clamp_min(1e-20)
+
+            def call():
+                ii, ww = _cpu_route(x, router, bias, F, torch)
                 moe_ref.moe_tokens_bf16(x, ii, ww, experts)
-                reps.append(time.perf_counter() - t1)
-            med = statistics.median(reps)
+            med = timed(call)
             tot_bytes += len(used) * per_expert
             tot_s += med
             tot_s_deq += med + t_deq
             done.append(f"L{l}/bs{T}")
     if tot_s == 0:
         return None
-    return {
+    out = {
         "value": tot_bytes / tot_s / 1e9,
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
+        "affinity_cores": affinity,
         "kind": "port",
         "sample": f"reference-faithful bf16 path (dequantise at load, bf16 F.linear per routed expert, "
-                  f"moe_tokens slot loop) on layers x batches {done}, median of 3 reps each; same "
-                  "algorithmic expert bytes as the GPU metric",
+                  f"moe_tokens slot loop) on layers x batches {done}, median of {CPU_REPS} reps "
+                  "each; same algorithmic expert bytes as the GPU metric",
         "dequant_inclusive_GBps": tot_bytes / tot_s_deq / 1e9,
         "torch": torch.__version__,
         "cpu_model": _cpu_model(),
     }
+    router, bias, stacks = _cpu_layer(layers[0], torch)
+    if prefill_tokens > 0:  # the full prefill batch, every routed expert dequantised at load
+        x = synth.make_tokens(prefill_tokens, seed=7).to(torch.bfloat16)
+        ids, _ = _cpu_route(x, router, bias, F, torch)
+        used = torch.unique(ids).tolist()
+        t_deq = time.perf_counter()
+        experts = _cpu_dequant(stacks, used, moe_ref, torch)
+        t_deq = time.perf_counter() - t_deq
+
+        def call_p():
+            ii, ww = _cpu_route(x, router, bias, F, torch)
+            moe_ref.moe_tokens_bf16(x, ii, ww, experts)
+        med = timed(call_p)
+        flops = synth.prefill_flops(prefill_tokens)
+        out["prefill"] = {"tokens": prefill_tokens, "layer_ms_p50": med * 1e3,
+                          "TFLOPs": flops / med / 1e12,
+                          "dequant_inclusive_layer_ms": (med + t_deq) * 1e3,
+                          "sample": f"layer 0 in full, median of {CPU_REPS} reps"}
+        log(f"[bench] cpu prefill T={prefill_tokens}: {med * 1e3:.1f} ms/layer "
+            f"({flops / med / 1e12:.3f} TFLOP/s) on {threads} threads")
+    if block_batches:  # the full block: routed experts plus the gated int4 shared expert
+        H = layers[0].experts.hidden_size
+        sh = synth.make_experts(1, H, layers[0].experts.intermediate_size, seed=4000)
+        shared = tuple(moe_ref.dequant_stack_torch(st.qweight, st.qzeros, st.scales)[0]
+                       for st in (sh.gate, sh.up, sh.down))
+        sgate = synth.make_shared_gate(H, seed=2500).view(1, H)
+        out["block"] = {}
+        for T in block_batches:
+            x = synth.make_tokens(T, seed=7).to(torch.bfloat16)
+            ids, _ = _cpu_route(x, router, bias, F, torch)
+            experts = _cpu_dequant(stacks, torch.unique(ids).tolist(), moe_ref, torch)
+
+            def call_b():
+                ii, ww = _cpu_route(x, router, bias, F, torch)
+                moe_ref.moe_tokens_bf16(x, ii, ww, experts, shared=shared, shared_gate_w=sgate)
+            med = timed(call_b)
+            out["block"][str(T)] = {"layer_us_p50": med * 1e6,
+                                    "sample": f"layer 0 with the shared expert, median of {CPU_REPS} reps"}
+    return out
 
 
 def _cpu_model() -> str:
