@@ -264,6 +264,37 @@ class OffloadedExperts:
         dst.copy_(blobs.reshape(-1))  # device -> pinned host DMA when the stack is on the GPU
         del blobs
 
+    def load_from_store(self, store, layer: int, *, store_layer: int | None = None,
+                        verify: bool = True) -> None:
+        """Fill pool layer `layer` from a repacked store (store layer `store_layer`, default the
+        same index): every expert's nine GPTQ tensors are copied from the layer file straight
+        into its blob in pinned host memory, after the manifest checks of
+        RepackedMoeExpertStore.read_layer_tensors (shape, dtype, sha256 with verify). The
+        store's g_idx must be k // group_size (the layout the kernels address)."""
+        src_layer = layer if store_layer is None else store_layer
+        t = store.read_layer_tensors(src_layer, verify=verify)
+        names = {"gate": "gate_proj", "up": "up_proj", "down": "down_proj"}
+        for proj, name in names.items():
+            gi = t[f"experts.{name}.g_idx"].to(torch.int64)
+            k = gi.shape[-1]
+            if gi.shape[0] != self.num_experts or not bool(
+                    (gi == torch.arange(k) // self.group_size).all()):
+                raise NotImplementedError(
+                    f"layer {src_layer} {name}: g_idx must be k // {self.group_size} for every "
+                    f"one of {self.num_experts} experts")
+        n = self.num_experts * self.blob
+        host = self.host.view()[layer * n:(layer + 1) * n].view(self.num_experts, self.blob)
+        for p in self.pieces:
+            src = t[f"experts.{names[p.proj]}.{p.kind}"]
+            if p.kind == "scales":
+                src = src.to(torch.float16)
+            if tuple(src.shape) != (self.num_experts,) + p.shape or src.dtype != p.dtype:
+                raise ValueError(f"layer {src_layer} {names[p.proj]}.{p.kind}: shape "
+                                 f"{tuple(src.shape)} {src.dtype} does not fit the pool "
+                                 f"({(self.num_experts,) + p.shape} {p.dtype})")
+            host[:, p.offset:p.offset + p.nbytes].copy_(
+                src.contiguous().view(torch.uint8).reshape(self.num_experts, p.nbytes))
+
     def prefetch(self, layer: int, experts, stream=None) -> int:
         return self.cache.prefetch(layer, experts, stream)
 

@@ -190,17 +190,64 @@ class RepackedMoeExpertStore:
             "checked_hashes": check_hashes,
         }
 
-    def load_layer(self, layer: int, *, device: str | torch.device = "cuda", group_size: int = 128):
-        """All experts of one layer as a device-resident MoeExperts (int4, repacked layout)."""
+    def read_layer_tensors(self, layer: int, *, verify: bool = True,
+                           projections: tuple[str, ...] = ("gate_proj", "up_proj", "down_proj"),
+                           kinds: tuple[str, ...] = ("qweight", "qzeros", "scales", "g_idx")
+                           ) -> dict[str, torch.Tensor]:
+        """The layer's stacked tensors {"experts.{proj}.{kind}": CPU tensor}, each checked
+        against its manifest record (shape, dtype and, with verify, the sha256 that
+        repack_layer wrote: qwen3_moe_gptq.py:112-118, 175-186). Raises ValueError on a
+        mismatch, naming the layer and key."""
+        out = {}
+        for proj in projections:
+            for kind in kinds:
+                info = self.tensor_info(layer, proj, kind)
+                t = self.get_fused_tensor(layer, proj, kind)
+                shape = tuple(int(d) for d in t.shape)
+                dtype = str(t.dtype).replace("torch.", "")
+                if shape != info.shape:
+                    raise ValueError(f"layer {layer} {info.key}: shape {list(shape)} != manifest "
+                                     f"{list(info.shape)}")
+                if dtype != info.dtype:
+                    raise ValueError(f"layer {layer} {info.key}: dtype {dtype} != manifest {info.dtype}")
+                if verify and info.sha256 is not None:
+                    digest = tensor_sha256(t)
+                    if digest != info.sha256:
+                        raise ValueError(f"layer {layer} {info.key}: sha256 {digest} != manifest "
+                                         f"{info.sha256}")
+                out[info.key] = t
+        return out
+
+    def load_layer(self, layer: int, *, device: str | torch.device = "cuda", group_size: int | None = None,
+                   verify: bool = True):
+        """All experts of one layer as a device-resident MoeExperts (int4, repacked layout),
+        verified against the manifest (read_layer_tensors) and copied host -> device through
+        pinned staging. g_idx must be k // group_size (checked by MoeExperts.validate); the
+        group size defaults to the one the tensors imply (in_features / scales rows)."""
         from mtp_amd.weights import GptqStack, MoeExperts
 
+        t = self.read_layer_tensors(layer, verify=verify)
+        dev = torch.device(device)
         stacks = {}
         for proj in ("gate_proj", "up_proj", "down_proj"):
-            t = {k: self.get_fused_tensor(layer, proj, k) for k in ("qweight", "qzeros", "scales", "g_idx")}
-            stacks[proj] = GptqStack(t["qweight"].to(device).contiguous(), t["qzeros"].to(device).contiguous(),
-                                     t["scales"].to(device=device, dtype=torch.float16).contiguous(),
-                                     t["g_idx"].to(device=device, dtype=torch.int32).contiguous())
-        return MoeExperts(stacks["gate_proj"], stacks["up_proj"], stacks["down_proj"], group_size)
+            moved = []
+            for kind in ("qweight", "qzeros", "scales", "g_idx"):
+                src = t[f"experts.{proj}.{kind}"]
+                if kind == "scales":
+                    src = src.to(torch.float16)
+                elif kind == "g_idx":
+                    src = src.to(torch.int32)
+                src = src.contiguous()
+                if dev.type == "cuda":
+                    src = src.pin_memory().to(dev, non_blocking=True)
+                moved.append(src)
+            stacks[proj] = GptqStack(*moved)
+        if group_size is None:
+            g = stacks["gate_proj"]
+            group_size = g.in_features // int(g.scales.shape[1])
+        experts = MoeExperts(stacks["gate_proj"], stacks["up_proj"], stacks["down_proj"], group_size)
+        experts.validate()
+        return experts
 
 
 def write_repacked_store(out_dir: str | Path, layers: dict[int, dict[str, torch.Tensor]],

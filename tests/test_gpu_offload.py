@@ -168,3 +168,47 @@ def test_prefetch_between_demand_and_kernels_keeps_demanded_slots(pooled):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     _slot_bytes_ok(pool, layer, demanded, pack_blobs(g.experts))
+
+
+def test_store_loads_into_hbm_stacks_and_the_pinned_pool(tmp_path):
+    """A written repacked store loaded two ways - load_layer (verified, HBM stacks) and
+    OffloadedExperts.load_from_store (verified, straight into the pinned host pool) - gives the
+    oracle's layer output; the pooled slots hold the same bytes as the resident stacks."""
+    from mtp_amd.repack import RepackedMoeExpertStore
+    from mtp_amd.repack.store import write_repacked_store
+    E, H, I = 16, 512, 256
+    lays = [small_layer(20 + l) for l in range(2)]
+    tensors = {}
+    for l, lay in enumerate(lays):
+        t = {}
+        for name, st in (("gate_proj", lay.experts.gate), ("up_proj", lay.experts.up),
+                         ("down_proj", lay.experts.down)):
+            t[f"experts.{name}.qweight"] = st.qweight
+            t[f"experts.{name}.qzeros"] = st.qzeros
+            t[f"experts.{name}.scales"] = st.scales
+            t[f"experts.{name}.g_idx"] = (torch.arange(st.in_features, dtype=torch.int32) // 128).repeat(E, 1)
+        tensors[l] = t
+    write_repacked_store(tmp_path, tensors, num_experts=E)
+    pool = OffloadedExperts(2, E, H, I, 6, group_size=128, device="cuda")
+    try:
+        with RepackedMoeExpertStore(tmp_path) as store:
+            for l in range(2):
+                _say(f"  store layer {l}")
+                resident = store.load_layer(l, device="cuda")
+                pool.load_from_store(store, l)
+                x = synth.make_tokens(3, H, seed=90 + l)
+                rng = np.random.default_rng(l)
+                ids = np.stack([rng.choice(E, 2, replace=False) for _ in range(3)]).astype(np.int32)
+                w = rng.uniform(0.2, 0.8, ids.shape).astype(np.float32)
+                idt, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+                pool.demand(l, ids.reshape(-1).tolist())
+                got_pool = ops.fused_experts(x.cuda(), idt, wt, pool.layer_experts(l), path="decode")
+                pool.layer_done(l)
+                got_res = ops.fused_experts(x.cuda(), idt, wt, resident, path="decode")
+                torch.cuda.synchronize()
+                assert torch.equal(got_pool, got_res)
+                _slot_bytes_ok(pool, l, ids.reshape(-1).tolist(), pack_blobs(resident))
+                ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(lays[l].experts))
+                assert moe_ref.rel_err(got_res.float().cpu().numpy(), ref) <= LAYER_RTOL
+    finally:
+        pool.close()

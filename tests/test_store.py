@@ -60,3 +60,29 @@ def test_synthetic_constants():
     assert synth.prefill_flops(2048) == 103_079_215_104
     b = synth.zipf_logit_bias(256, seed=3000)
     assert b.shape == (256,) and torch.isfinite(b).all()
+
+
+def test_load_layer_verifies_the_manifest_on_load(tmp_path):
+    """load_layer / read_layer_tensors check every tensor against the manifest (shape, dtype,
+    sha256) before anything is copied; a corrupted tensor is refused by name."""
+    tensors = _layer_tensors()
+    write_repacked_store(tmp_path, {0: tensors}, num_experts=4)
+    with RepackedMoeExpertStore(tmp_path) as store:
+        ex = store.load_layer(0, device="cpu")
+        assert ex.group_size == 128 and ex.gate.num_rows == 4
+        assert torch.equal(ex.down.qzeros, tensors["experts.down_proj.qzeros"])
+    bad = dict(tensors)
+    q = tensors["experts.gate_proj.qweight"].clone()
+    q[1, 3, 5] ^= 1  # one bit of one packed word
+    bad["experts.gate_proj.qweight"] = q
+    from safetensors.torch import save_file
+    save_file(bad, str(tmp_path / "layer_00.safetensors"))
+    with RepackedMoeExpertStore(tmp_path) as store:
+        with pytest.raises(ValueError, match="experts.gate_proj.qweight: sha256"):
+            store.load_layer(0, device="cpu")
+        assert store.load_layer(0, device="cpu", verify=False).gate.num_rows == 4
+    bad["experts.gate_proj.qweight"] = q[:, :-1].contiguous()  # a shape the manifest does not list
+    save_file(bad, str(tmp_path / "layer_00.safetensors"))
+    with RepackedMoeExpertStore(tmp_path) as store:
+        with pytest.raises(ValueError, match="shape"):
+            store.read_layer_tensors(0, verify=False)
