@@ -204,6 +204,41 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
 
 /* ---------------------------------------------------------------- expert-demand predictor */
 
+/* Parameters of the reference's HiddenResidualExpertPredictor
+ * (src/mtp_expert_prefetch/training/hidden_residual.py:44-106) in bf16 (biases as fp32 holding
+ * bf16 values): encoder = Linear(hidden, width) -> SiLU -> LayerNorm(width) (key names
+ * encoder.0.*, encoder.2.*), layer_embedding [num_layers, width], delta_embedding
+ * [future_window, width], classifier = Linear(width, num_experts). */
+typedef struct moe_hr_predictor_params_v1 {
+  const uint16_t* enc_w;      /* bf16 [width, hidden] */
+  const float* enc_b;         /* fp32 [width] */
+  const uint16_t* ln_w;       /* bf16 [width] */
+  const uint16_t* ln_b;       /* bf16 [width] */
+  const uint16_t* layer_emb;  /* bf16 [num_layers, width] */
+  const uint16_t* delta_emb;  /* bf16 [future_window, width] */
+  const uint16_t* cls_w;      /* bf16 [num_experts, width] */
+  const float* cls_b;         /* fp32 [num_experts] */
+  int32_t hidden, width, num_layers, future_window, num_experts;
+  float ln_eps;
+} moe_hr_predictor_params_v1;
+
+/* Workspace bytes of moe_hr_predictor_v1 for N examples (-1 on bad arguments). */
+int64_t moe_hr_predictor_workspace_bytes_v1(int32_t N, const moe_hr_predictor_params_v1* params);
+
+/* HiddenResidualExpertPredictor.forward(hidden [N, hidden] bf16, layer_ids [N] int32) ->
+ * residual [N, future_window, num_experts], combined as out = prior + scale * residual
+ * (train_hidden_residual_predictor_smoke.py:446; prior NULL = 0; scale = scale_per_example[n]
+ * when given, else residual_scale, as apply_residual_scale :108-121 with a fixed or learnt
+ * gamma), and the top_k experts of every (example, delta) row by (value, lower id).
+ * Activations between the Linear layers are bf16; the dot products use the router's canonical
+ * fp32 order. A layer id outside [0, num_layers) reads a zero embedding. logits_out: NULL or
+ * fp32 [N, future_window, num_experts]; topk_ids int32 [N, future_window, top_k]. */
+int moe_hr_predictor_v1(const uint16_t* hidden, int32_t N, const int32_t* layer_ids,
+                        const moe_hr_predictor_params_v1* params, const float* prior,
+                        float residual_scale, const float* scale_per_example, int32_t top_k,
+                        void* workspace, int64_t workspace_bytes, float* logits_out,
+                        int32_t* topk_ids, void* stream);
+
 /* Workspace bytes of moe_predictor_v1. */
 int64_t moe_predictor_workspace_bytes_v1(int32_t T, int32_t num_heads, int32_t inner,
                                          int32_t num_experts, int32_t top_k);
@@ -238,7 +273,8 @@ typedef struct moe_slot_cache_desc_v1 {
   int32_t* device_expert_row; /* device [num_layers][num_experts]: expert -> slot, -1 when not
                                resident (its slots are dropped); the caller initialises it */
   int32_t dry_run;
-  int32_t reserved;
+  float ready_deadline_us;    /* a prefetched expert is ready-late when its copy completes more
+                               than this after the demand that first uses it */
 } moe_slot_cache_desc_v1;
 
 /* Counters with the semantics of ControlledExpertCacheManager
@@ -256,6 +292,13 @@ typedef struct moe_slot_cache_counters_v1 {
   int64_t prefetch_bytes;
   int64_t demand_bytes;
   int64_t prefetch_skipped_pinned_count; /* prefetches not issued: every slot was pinned */
+  /* ReadyTimeExpertCacheManager (cache_manager.py:298-578) on real transfers: first demands of a
+   * prefetched expert whose copy completed after the demand (+ ready_deadline_us), measured
+   * with HIP event timestamps, and their total lateness. The reference counts such a demand as
+   * a miss (ready_late_miss_count); here the layer waits for the copy, so the data counters
+   * above still count it as a hit. */
+  int64_t ready_late_miss_count;
+  int64_t ready_late_wait_ns;
 } moe_slot_cache_counters_v1;
 
 /* Opaque handle (a magic field is checked on every call). Not thread-safe. */

@@ -48,6 +48,8 @@ EXPORTED = (
     "moe_layer_noalloc_v1",
     "moe_predictor_workspace_bytes_v1",
     "moe_predictor_v1",
+    "moe_hr_predictor_workspace_bytes_v1",
+    "moe_hr_predictor_v1",
     "moe_slot_cache_create_v1",
     "moe_slot_cache_destroy_v1",
     "moe_slot_cache_prefetch_v1",
@@ -69,7 +71,7 @@ class SlotCacheDesc(ctypes.Structure):
         ("device_pool", c_void_p),
         ("device_expert_row", c_void_p),
         ("dry_run", c_int32),
-        ("reserved", c_int32),
+        ("ready_deadline_us", c_float),
     ]
 
 
@@ -78,7 +80,14 @@ class SlotCacheCounters(ctypes.Structure):
         "capacity", "resident_count", "issued_fetch_count", "used_fetch_count",
         "unused_fetch_count", "demand_count", "demand_hit_count", "demand_miss_count",
         "evicted_before_use_count", "prefetch_bytes", "demand_bytes",
-        "prefetch_skipped_pinned_count")]
+        "prefetch_skipped_pinned_count", "ready_late_miss_count", "ready_late_wait_ns")]
+
+
+class HrPredictorParams(ctypes.Structure):
+    _fields_ = [(name, c_void_p) for name in (
+        "enc_w", "enc_b", "ln_w", "ln_b", "layer_emb", "delta_emb", "cls_w", "cls_b")] + [
+        (name, c_int32) for name in ("hidden", "width", "num_layers", "future_window",
+                                     "num_experts")] + [("ln_eps", c_float)]
 
 
 class GptqProj(ctypes.Structure):
@@ -138,6 +147,9 @@ _SIGS = {
         c_int32),
     "moe_predictor_workspace_bytes_v1": ([_I, _I, _I, _I, _I], c_int64),
     "moe_predictor_v1": ([_P, _I, _I, _I, _P, _I, _P, _I, _I, _P, c_int64, _P, _P], c_int32),
+    "moe_hr_predictor_workspace_bytes_v1": ([_I, POINTER(HrPredictorParams)], c_int64),
+    "moe_hr_predictor_v1": ([_P, _I, _P, POINTER(HrPredictorParams), _P, c_float, _P, _I, _P, c_int64,
+                             _P, _P, _P], c_int32),
     "moe_slot_cache_create_v1": ([POINTER(SlotCacheDesc), POINTER(ctypes.c_uint64)], c_int32),
     "moe_slot_cache_destroy_v1": ([ctypes.c_uint64], c_int32),
     "moe_slot_cache_prefetch_v1": ([ctypes.c_uint64, _I, _P, _I, _P, POINTER(c_int32)], c_int32),

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "moe_w4a16.h"
+
 // Thread-local message of the last failed entry point (moe_w4a16_last_error).
 constexpr int kErrorBufferBytes = 512;
 char* moe_error_buffer();
@@ -144,3 +146,10 @@ hipError_t launch_rmsnorm(uint16_t* res, const uint16_t* add, int T, int H, cons
 // Block sizes (slots per block) of the two paths.
 constexpr int kDecodeBlockM = 16;
 constexpr int kPrefillBlockM = 128;
+
+// HiddenResidualExpertPredictor forward (hr_predictor.hip).
+int64_t hr_predictor_workspace(int N, int W, int F, int E);
+hipError_t launch_hr_predictor(const uint16_t* x, int N, int H, const int32_t* layer_ids,
+                               const moe_hr_predictor_params_v1& p, const float* prior, float scale,
+                               const float* scale_per_example, int top_k, void* workspace,
+                               float* out, int32_t* ids, hipStream_t stream);

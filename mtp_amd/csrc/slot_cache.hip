@@ -20,6 +20,14 @@
 //    stream, so an unpinned slot is never overwritten while an enqueued kernel may read it.
 // The table entry of an absent expert is -1: the kernels drop the slots routed to it (they
 // contribute zero). Handles are not thread-safe: one handle per host thread.
+//
+// Ready-time accounting (the reference's ReadyTimeExpertCacheManager, cache_manager.py:298-578,
+// on real transfers): every prefetch call records a timing event on the side stream after its
+// copies, and every demand records one on the compute stream when it is issued (after the work
+// already enqueued there, i.e. when the layer needs its experts). The first demand of a
+// prefetched expert is ready-late when its copy completed more than ready_deadline_us after the
+// demand's event: the compute stream then waits for the copy. The elapsed time between the two
+// events settles it once both have completed (polled at every call, waited for by stats).
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -35,6 +43,7 @@ namespace {
 
 constexpr uint64_t kMagic = 0x4D4F45534C4F5431ull;  // "MOESLOT1"
 constexpr int kStagingRing = 512;
+constexpr int kEventRing = 1024;  // timing events of prefetch calls and of demands
 
 struct Slot {
   int expert = -1;
@@ -42,6 +51,12 @@ struct Slot {
   bool used = false;
   bool pinned = false;  // named by the layer's latest demand; its kernels may not be enqueued yet
   uint64_t last_use = 0;
+  uint64_t pf_seq = 0;  // prefetch call whose copy filled the slot (0: none)
+};
+
+// A prefetched expert's first demand, settled when both events have completed.
+struct ReadyCheck {
+  uint64_t pf_seq, dm_seq;
 };
 
 struct Layer {
@@ -61,6 +76,9 @@ struct Cache {
   int32_t* staging = nullptr;  // pinned [kStagingRing][num_experts]
   std::vector<hipEvent_t> staging_done;
   int staging_next = 0;
+  std::vector<hipEvent_t> pf_ev, dm_ev;  // timing events, rings of kEventRing
+  uint64_t pf_seq = 0, dm_seq = 0;       // calls recorded so far (sequence numbers from 1)
+  std::vector<ReadyCheck> checks;        // unsettled first demands, oldest first
   moe_slot_cache_counters_v1 st{};
 };
 
@@ -128,6 +146,33 @@ void evict(Cache* c, Layer& L, int s) {
   sl = Slot{};
 }
 
+// Settles the ready checks whose events have completed (all of them when wait is set, and
+// always those that name an event slot about to be reused by reuse_pf / reuse_dm).
+int settle(Cache* c, bool wait, uint64_t reuse_pf = 0, uint64_t reuse_dm = 0) {
+  std::vector<ReadyCheck> open;
+  for (const ReadyCheck& k : c->checks) {
+    hipEvent_t pe = c->pf_ev[k.pf_seq % kEventRing], de = c->dm_ev[k.dm_seq % kEventRing];
+    const bool must = wait || k.pf_seq + kEventRing <= reuse_pf || k.dm_seq + kEventRing <= reuse_dm;
+    if (must) {
+      SC_HIP(hipEventSynchronize(pe), "ready check");
+      SC_HIP(hipEventSynchronize(de), "ready check");
+    } else if (hipEventQuery(pe) != hipSuccess || hipEventQuery(de) != hipSuccess) {
+      (void)hipGetLastError();  // "not ready" is an answer, not an error to report later
+      open.push_back(k);
+      continue;
+    }
+    float ms = 0.0f;  // copy completion relative to the demand: > 0 means it arrived later
+    SC_HIP(hipEventElapsedTime(&ms, de, pe), "ready check time");
+    const double late_us = (double)ms * 1e3 - (double)c->d.ready_deadline_us;
+    if (late_us > 0.0) {
+      c->st.ready_late_miss_count++;
+      c->st.ready_late_wait_ns += (int64_t)(late_us * 1e3);
+    }
+  }
+  c->checks.swap(open);
+  return MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -160,6 +205,10 @@ int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handl
     c->staging_done.assign(kStagingRing, nullptr);
     for (hipEvent_t& e : c->staging_done)
       SC_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "create event");
+    c->pf_ev.assign(kEventRing, nullptr);
+    c->dm_ev.assign(kEventRing, nullptr);
+    for (hipEvent_t& e : c->pf_ev) SC_HIP(hipEventCreate(&e), "create timing event");
+    for (hipEvent_t& e : c->dm_ev) SC_HIP(hipEventCreate(&e), "create timing event");
   }
   *handle = reinterpret_cast<uint64_t>(c);
   return MOE_OK;
@@ -173,6 +222,8 @@ int moe_slot_cache_destroy_v1(uint64_t handle) {
     hipStreamSynchronize(c->side);
     for (Layer& L : c->layers) hipEventDestroy(L.prefetch_done);
     for (hipEvent_t e : c->staging_done) hipEventDestroy(e);
+    for (hipEvent_t e : c->pf_ev) hipEventDestroy(e);
+    for (hipEvent_t e : c->dm_ev) hipEventDestroy(e);
     hipEventDestroy(c->compute_mark);
     hipStreamDestroy(c->side);
     hipHostFree(c->staging);
@@ -212,7 +263,7 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
     }
     c->st.issued_fetch_count++;
     evict(c, L, s);
-    L.slots[s] = Slot{e, true, false, false, ++c->tick};
+    L.slots[s] = Slot{e, true, false, false, ++c->tick, live(c) ? c->pf_seq + 1 : 0};
     L.slot_of[e] = s;
     ++count;
     if (live(c)) {
@@ -229,6 +280,10 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
   if (count > 0 && live(c)) {
     SC_HIP(hipEventRecord(L.prefetch_done, c->side), "record prefetch done");
     L.pending = true;
+    const uint64_t seq = ++c->pf_seq;  // the slots filled above carry this number
+    int rc = settle(c, false, seq, 0);
+    if (rc) return rc;
+    SC_HIP(hipEventRecord(c->pf_ev[seq % kEventRing], c->side), "record prefetch time");
   }
   if (issued) *issued = count;
   return MOE_OK;
@@ -258,6 +313,13 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
   // The previous demand's kernels were enqueued on the compute stream before this call, so
   // its pins can go: this demand's copies and the prefetches after it are ordered after them.
   unpin(L);
+  uint64_t dseq = 0;
+  if (live(c)) {  // when the layer needs its experts: after the work already on the stream
+    dseq = ++c->dm_seq;
+    int rc = settle(c, false, 0, dseq);
+    if (rc) return rc;
+    SC_HIP(hipEventRecord(c->dm_ev[dseq % kEventRing], cs), "record demand time");
+  }
   if (L.pending && live(c)) {
     SC_HIP(hipStreamWaitEvent(cs, L.prefetch_done, 0), "compute waits prefetch");
     L.pending = false;
@@ -271,7 +333,10 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
       c->st.demand_hit_count++;
       ++nh;
       Slot& sl = L.slots[s];
-      if (sl.prefetched && !sl.used) c->st.used_fetch_count++;
+      if (sl.prefetched && !sl.used) {
+        c->st.used_fetch_count++;
+        if (dseq && sl.pf_seq) c->checks.push_back(ReadyCheck{sl.pf_seq, dseq});
+      }
       sl.used = true;
       sl.pinned = true;
       sl.last_use = ++c->tick;
@@ -283,7 +348,7 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
     // this call already touched (those hold the newest ticks).
     s = pick_slot(L, false);
     evict(c, L, s);
-    L.slots[s] = Slot{e, false, true, true, ++c->tick};
+    L.slots[s] = Slot{e, false, true, true, ++c->tick, 0};
     L.slot_of[e] = s;
     if (live(c)) {
       SC_HIP(hipMemcpyAsync(device_slot(c, layer, s), host_blob(c, layer, e), c->d.expert_bytes,
@@ -318,6 +383,10 @@ int moe_slot_cache_layer_done_v1(uint64_t handle, int32_t layer) {
 int moe_slot_cache_stats_v1(uint64_t handle, moe_slot_cache_counters_v1* out) {
   Cache* c = from_handle(handle);
   if (!c || !out) return fail(MOE_ERR_NULL, "slot cache: bad handle or NULL output");
+  if (live(c)) {
+    int rc = settle(c, true);
+    if (rc) return rc;
+  }
   moe_slot_cache_counters_v1 s = c->st;
   int64_t resident = 0, unused = 0;
   for (const Layer& L : c->layers)

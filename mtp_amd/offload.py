@@ -124,10 +124,11 @@ class SlotCache:
 
     def __init__(self, num_layers: int, num_experts: int, slots_per_layer: int, expert_bytes: int,
                  *, host_pool: int = 0, device_pool: int = 0, expert_row: int = 0,
-                 device: int = 0, dry_run: bool = False) -> None:
+                 device: int = 0, dry_run: bool = False, ready_deadline_us: float = 0.0) -> None:
         self._lib = _lib.load()
         desc = _lib.SlotCacheDesc(num_layers, num_experts, slots_per_layer, device, expert_bytes,
-                                  host_pool, device_pool, expert_row, int(dry_run), 0)
+                                  host_pool, device_pool, expert_row, int(dry_run),
+                                  float(ready_deadline_us))
         handle = ctypes.c_uint64()
         _lib.check(self._lib.moe_slot_cache_create_v1(ctypes.byref(desc), ctypes.byref(handle)))
         self.handle = handle.value

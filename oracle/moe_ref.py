@@ -303,3 +303,51 @@ def rmsnorm_ref(res_bits: np.ndarray, weight_bits: np.ndarray, *, add_bits: np.n
     w1 = (np.float32(1.0) + gptq_ref.bf16_bits_to_f32(weight_bits)).astype(np.float32)
     out = ((x * r).astype(np.float32) * w1).astype(np.float32)
     return gptq_ref.f32_to_bf16_bits(x), gptq_ref.f32_to_bf16_bits(out)
+
+
+# --------------------------------------------------------------------------- hidden-residual predictor
+def _bf16r(v: np.ndarray) -> np.ndarray:
+    return gptq_ref.bf16_bits_to_f32(gptq_ref.f32_to_bf16_bits(np.asarray(v, dtype=np.float32)))
+
+
+def hidden_residual_ref(h_bits: np.ndarray, p: dict, layer_ids: np.ndarray, *, top_k: int,
+                        prior: np.ndarray | None = None, scale: float = 1.0,
+                        scale_per_example: np.ndarray | None = None, ln_eps: float = 1e-5):
+    """HiddenResidualExpertPredictor.forward (training/hidden_residual.py:44-106) with bf16
+    activations between its Linear layers, the residual combination prior + scale * residual
+    (scripts/train_hidden_residual_predictor_smoke.py:446) and the stable top-k per row.
+
+    p: enc_w / ln_w / ln_b / layer_emb / delta_emb / cls_w as bf16 bits, enc_b / cls_b fp32.
+    Steps (fp32 unless rounded): z = bf16(canonical(x, W_enc) + b_enc); a = bf16(silu(z));
+    s = bf16(LayerNorm(a) * ln_w + ln_b) with float64 statistics rounded to fp32;
+    c_d = bf16(bf16(s + E_layer[l]) + E_delta[d]); g_d = bf16(silu(c_d));
+    r = canonical(g, W_cls) + b_cls. Returns (ids [N, F, k], out [N, F, E], residual [N, F, E])."""
+    h = gptq_ref.bf16_bits_to_f32(h_bits)
+    N = h.shape[0]
+    enc_w = gptq_ref.bf16_bits_to_f32(p["enc_w"])
+    W = enc_w.shape[0]
+    z = _bf16r(canonical_dot_rows(h, enc_w) + p["enc_b"].astype(np.float32)[None, :])
+    a = _bf16r(z / (np.float32(1.0) + np.exp(-z)))
+    mean = a.astype(np.float64).mean(axis=1, keepdims=True).astype(np.float32)
+    var = ((a - mean).astype(np.float64) ** 2).mean(axis=1, keepdims=True).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt(var + np.float32(ln_eps))).astype(np.float32)
+    s = _bf16r(((a - mean) * rstd).astype(np.float32) * gptq_ref.bf16_bits_to_f32(p["ln_w"])[None, :]
+               + gptq_ref.bf16_bits_to_f32(p["ln_b"])[None, :])
+    lemb = gptq_ref.bf16_bits_to_f32(p["layer_emb"])
+    ok = (layer_ids >= 0) & (layer_ids < lemb.shape[0])
+    le = np.where(ok[:, None], lemb[np.clip(layer_ids, 0, lemb.shape[0] - 1)], np.float32(0.0))
+    sl = _bf16r(s + le)
+    demb = gptq_ref.bf16_bits_to_f32(p["delta_emb"])
+    F = demb.shape[0]
+    c = _bf16r(sl[:, None, :] + demb[None, :, :])
+    g = _bf16r(c / (np.float32(1.0) + np.exp(-c)))
+    cls_w = gptq_ref.bf16_bits_to_f32(p["cls_w"])
+    E = cls_w.shape[0]
+    r = (canonical_dot_rows(g.reshape(N * F, W), cls_w) + p["cls_b"].astype(np.float32)[None, :])
+    r = r.astype(np.float32).reshape(N, F, E)
+    sc = (np.asarray(scale_per_example, dtype=np.float32)[:, None, None] if scale_per_example is not None
+          else np.float32(scale))
+    base = np.zeros_like(r) if prior is None else prior.astype(np.float32)
+    out = (base + (sc * r).astype(np.float32)).astype(np.float32)
+    ids = stable_topk(out.reshape(N * F, E), top_k).reshape(N, F, top_k)
+    return ids, out, r

@@ -212,3 +212,122 @@ def test_store_loads_into_hbm_stacks_and_the_pinned_pool(tmp_path):
                 assert moe_ref.rel_err(got_res.float().cpu().numpy(), ref) <= LAYER_RTOL
     finally:
         pool.close()
+
+
+def _hr_oracle_params(m):
+    b = lambda t: bf16_bits(t)  # noqa: E731
+    return {"enc_w": b(m.enc_w), "enc_b": m.enc_b.cpu().numpy(), "ln_w": b(m.ln_w),
+            "ln_b": b(m.ln_b), "layer_emb": b(m.layer_emb), "delta_emb": b(m.delta_emb),
+            "cls_w": b(m.cls_w), "cls_b": m.cls_b.cpu().numpy()}
+
+
+def _ids_match_up_to_near_ties(got, want, logits, atol):
+    g, w, lg = got.reshape(-1, got.shape[-1]), want.reshape(-1, want.shape[-1]), logits.reshape(-1, logits.shape[-1])
+    for r in range(g.shape[0]):
+        for j in range(g.shape[1]):
+            a, b = int(g[r, j]), int(w[r, j])
+            if a != b:
+                assert abs(float(lg[r, a]) - float(lg[r, b])) <= atol, (r, j, a, b)
+
+
+@pytest.mark.parametrize("scope", ["fixed", "layer"])
+def test_hidden_residual_predictor_matches_oracle(scope):
+    """The reference's HiddenResidualExpertPredictor at its default shape (hidden 2048, width
+    256, 40 layers, 4 future deltas, 256 experts) on the HIP kernels against the oracle:
+    residual and combined logits within bf16-activation tolerance, top-16 ids equal up to
+    near-ties."""
+    from mtp_amd.predictor import HiddenResidualExpertPredictor
+    _say(f"hidden-residual predictor scope={scope}")
+    m = HiddenResidualExpertPredictor(seed=5, learnable_residual_gamma=(scope == "layer"),
+                                      residual_gamma_scope="layer" if scope == "layer" else "scalar",
+                                      initial_residual_gamma=0.8)
+    if scope == "layer":
+        m.raw_residual_gamma.data.copy_(torch.linspace(-1.0, 1.0, 40, device="cuda"))
+    g = torch.Generator().manual_seed(6)
+    N = 5
+    h = torch.randn(N, 2048, generator=g).to(torch.bfloat16)
+    lid = torch.tensor([0, 39, 7, 7, 20], dtype=torch.int32)
+    prior = torch.randn(N, 4, 256, generator=g)
+    ids, out = m.predict_topk(h.cuda(), layer_ids=lid, k=16, prior=prior, fixed_scale=0.7,
+                              return_logits=True)
+    resid = m(h.cuda(), layer_ids=lid)
+    torch.cuda.synchronize()
+    p = _hr_oracle_params(m)
+    per = None
+    if scope == "layer":
+        per = torch.nn.functional.softplus(torch.linspace(-1.0, 1.0, 40))[lid.long()].numpy()
+    r_ids, r_out, r_res = moe_ref.hidden_residual_ref(bf16_bits(h), p, lid.numpy(), top_k=16,
+                                                      prior=prior.numpy(), scale=0.7,
+                                                      scale_per_example=per)
+    atol = 5e-3
+    assert np.max(np.abs(resid.cpu().numpy() - r_res)) <= atol
+    assert np.max(np.abs(out.cpu().numpy() - r_out)) <= atol * 2
+    _ids_match_up_to_near_ties(ids.cpu().numpy(), r_ids, r_out, 4 * atol)
+    with pytest.raises(ValueError, match="layer_ids must have shape"):
+        m(h.cuda(), layer_ids=lid[:2])
+
+
+def test_hidden_residual_predictor_loads_a_reference_state_dict():
+    """Parameters in the reference module's state_dict names: the forward then agrees with the
+    same architecture built from torch's layers in fp32 (to bf16 accuracy)."""
+    from mtp_amd.predictor import HiddenResidualExpertPredictor
+    H, W, L, Fw, E = 512, 128, 6, 3, 64
+    torch.manual_seed(3)
+    enc = torch.nn.Sequential(torch.nn.Linear(H, W), torch.nn.SiLU(), torch.nn.LayerNorm(W))
+    lemb, demb, cls = torch.nn.Embedding(L, W), torch.nn.Embedding(Fw, W), torch.nn.Linear(W, E)
+    with torch.no_grad():  # bf16-representable parameters, as a bf16 checkpoint holds them
+        for mod in (enc[0], enc[2], lemb, demb, cls):
+            for prm in mod.parameters():
+                prm.copy_(prm.to(torch.bfloat16).float())
+    state = {"encoder.0.weight": enc[0].weight, "encoder.0.bias": enc[0].bias,
+             "encoder.2.weight": enc[2].weight, "encoder.2.bias": enc[2].bias,
+             "layer_embedding.weight": lemb.weight, "delta_embedding.weight": demb.weight,
+             "classifier.weight": cls.weight, "classifier.bias": cls.bias}
+    m = HiddenResidualExpertPredictor(hidden_size=H, num_experts=E, num_layers=L,
+                                      future_window=Fw, width=W)
+    m.load_reference_state_dict(state)
+    h = torch.randn(4, H).to(torch.bfloat16)
+    lid = torch.tensor([0, 5, 2, 2])
+    got = m(h.cuda(), layer_ids=lid).cpu().numpy()
+    with torch.no_grad():
+        st = enc(h.float())
+        ctx = st[:, None, :] + lemb(lid)[:, None, :] + demb(torch.arange(Fw))[None, :, :]
+        want = cls(torch.nn.functional.silu(ctx)).numpy()
+    assert moe_ref.rel_err(got, want) < 2e-2
+
+
+def test_ready_late_first_demands_are_counted_from_event_times():
+    """Prefetches still in flight when the layer demands them are ready-late (the copy completes
+    after the demand's event); prefetches that completed first are not. The layer output stays
+    exact either way (the demand waits for the copies)."""
+    E, H, I = 16, 2048, 512
+    ex = synth.make_experts(E, H, I, seed=77, device="cuda")
+    pool = OffloadedExperts(1, E, H, I, 8, group_size=128, device="cuda")
+    try:
+        pool.store_layer(0, ex)
+        torch.cuda.synchronize()
+        # completed before the demand: not late
+        pool.prefetch(0, [0, 1])
+        torch.cuda.synchronize()
+        pool.demand(0, [0, 1])
+        pool.layer_done(0)
+        torch.cuda.synchronize()
+        st = pool.stats()
+        assert st["ready_late_miss_count"] == 0 and st["demand_hit_count"] == 2
+        # six 1.6 MB copies queued right before the demand: the later ones complete after it
+        pool.prefetch(0, [2, 3, 4, 5, 6, 7])
+        pool.demand(0, [2, 3, 4, 5, 6, 7])
+        x = synth.make_tokens(1, H, seed=3).cuda()
+        ids = torch.tensor([[2, 3, 4, 5, 6, 7]], dtype=torch.int32, device="cuda")
+        w = torch.full((1, 6), 1.0 / 6, device="cuda")
+        got = ops.fused_experts(x, ids, w, pool.layer_experts(0), path="decode")
+        pool.layer_done(0)
+        want = ops.fused_experts(x, ids, w, ex, path="decode")
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        st = pool.stats()
+        _say(f"  ready-late {st['ready_late_miss_count']} of 6, wait {st['ready_late_wait_ns'] / 1e3:.1f} us")
+        assert st["ready_late_miss_count"] >= 1 and st["ready_late_wait_ns"] > 0
+        assert st["demand_hit_count"] == 8
+    finally:
+        pool.close()
