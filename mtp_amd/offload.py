@@ -354,19 +354,35 @@ class OffloadDecoder:
         self.pool, self.routers, self.biases = pool, routers, biases
         self.top_k, self.path, self.prefetch_k = top_k, path, prefetch_k
         self.predictor = predictor
-        if predictor is not None:
+        if isinstance(predictor, tuple):
             w1, w2 = predictor
             if w1.shape[0] != pool.num_layers or w2.shape[0] != pool.num_layers:
                 raise ValueError("predictor needs one head per layer")
+        elif predictor is not None and predictor.num_layers < pool.num_layers:
+            raise ValueError("the predictor's layer embedding covers fewer layers than the pool")
         self._ids_host: torch.Tensor | None = None
         self._pred_host: torch.Tensor | None = None
         self._ws: torch.Tensor | None = None
         self._pred_ws: torch.Tensor | None = None
 
     def predict(self, h: torch.Tensor) -> list[list[int]]:
-        """Per layer, the distinct experts of the predictor's top-prefetch_k over h's rows."""
+        """Per layer, the distinct experts of the predictor's top-prefetch_k over h's rows.
+
+        The predictor is either per-layer MLP heads (w1 [L, D, H], w2 [L, E, D]) or a
+        HiddenResidualExpertPredictor, whose next-token delta (0) row for layer l is used."""
         if self.predictor is None or self.prefetch_k <= 0:
             return [[] for _ in range(self.pool.num_layers)]
+        if not isinstance(self.predictor, tuple):
+            L, T = self.pool.num_layers, h.shape[0]
+            hh = h.repeat(L, 1)  # example (l, t) = row l * T + t
+            lid = torch.arange(L, dtype=torch.int32, device=h.device).repeat_interleave(T)
+            ids = self.predictor.predict_topk(hh, layer_ids=lid, k=self.prefetch_k)[:, 0, :]
+            if self._pred_host is None or self._pred_host.shape != ids.shape:
+                self._pred_host = torch.empty(ids.shape, dtype=torch.int32, pin_memory=True)
+            self._pred_host.copy_(ids, non_blocking=True)
+            torch.cuda.current_stream().synchronize()
+            per = self._pred_host.view(L, T * self.prefetch_k)
+            return [list(dict.fromkeys(per[l].tolist())) for l in range(L)]
         w1, w2 = self.predictor
         L, T, k = self.pool.num_layers, h.shape[0], self.prefetch_k
         need = ops.predictor_workspace_bytes(T, L, w1.shape[1], w2.shape[1], k)
