@@ -202,6 +202,24 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
                          const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
                          uint16_t* out, int32_t path, void* stream);
 
+/* ---------------------------------------------------------------- AWQ checkpoints */
+#define MOE_AWQ_WNA16 1 /* vLLM int4 fused-MoE layout: uint8 [E, N, K/2], zeros uint8 [E, N/2, K/G] */
+#define MOE_AWQ_GEMM 2  /* AutoAWQ GEMM: int32 [E, K, N/8] and [E, K/G, N/8], order 0,2,4,6,1,3,5,7 */
+
+/* Exact repack of AWQ int4 experts into the GPTQ layout the kernels read (out: caller-allocated
+ * device qweight int32 [E, K/8, N], qzeros int32 [E, K/G, N/8], scales fp16 [E, K/G, N]).
+ * Replaces the AWQ weight path of the reference's production run (vLLM wna16,
+ * src/mtp_expert_prefetch/tracing/vllm_wna16_group_plan.py:394-470;
+ * configs/model/qwen3_6_35b_a3b_awq_4bit.yaml): every (q - z) * s is unchanged. layout
+ * MOE_AWQ_WNA16: qzeros NULL = symmetric (zero 8); scales [E, N, K/G] fp16 or bf16
+ * (scales_bf16 = 1). MOE_AWQ_GEMM: qweight int32 [E, K, N/8], qzeros int32 [E, K/G, N/8],
+ * scales fp16 [E, K/G, N]. *status (device int32) is 0 when every value moved exactly, 1 when
+ * a bf16 scale has no exact fp16 value (outside [2^-17, 65504]). Stream-ordered. */
+int moe_awq_to_gptq_v1(int32_t layout, const void* qweight, const void* qzeros,
+                       const uint16_t* scales, int32_t scales_bf16, int32_t num_experts,
+                       int32_t in_features, int32_t out_features, int32_t group_size,
+                       const moe_gptq_proj_v1* out, int32_t* status, void* stream);
+
 /* ---------------------------------------------------------------- expert-demand predictor */
 
 /* Parameters of the reference's HiddenResidualExpertPredictor

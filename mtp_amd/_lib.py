@@ -48,6 +48,7 @@ EXPORTED = (
     "moe_layer_noalloc_v1",
     "moe_predictor_workspace_bytes_v1",
     "moe_predictor_v1",
+    "moe_awq_to_gptq_v1",
     "moe_hr_predictor_workspace_bytes_v1",
     "moe_hr_predictor_v1",
     "moe_slot_cache_create_v1",
@@ -147,6 +148,7 @@ _SIGS = {
         c_int32),
     "moe_predictor_workspace_bytes_v1": ([_I, _I, _I, _I, _I], c_int64),
     "moe_predictor_v1": ([_P, _I, _I, _I, _P, _I, _P, _I, _I, _P, c_int64, _P, _P], c_int32),
+    "moe_awq_to_gptq_v1": ([_I, _P, _P, _P, _I, _I, _I, _I, _I, POINTER(GptqProj), _P, _P], c_int32),
     "moe_hr_predictor_workspace_bytes_v1": ([_I, POINTER(HrPredictorParams)], c_int64),
     "moe_hr_predictor_v1": ([_P, _I, _P, POINTER(HrPredictorParams), _P, c_float, _P, _I, _P, c_int64,
                              _P, _P, _P], c_int32),

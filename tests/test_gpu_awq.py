@@ -1,0 +1,105 @@
+"""AWQ checkpoints on the GPU: the repack kernel against the oracle (bit-exact GPTQ tensors for
+the vLLM wna16 and AutoAWQ GEMM layouts, with and without zero points, fp16 and bf16 scales) and
+a layer on AWQ-sourced experts against the oracle layer."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mtp_amd import ops, synth
+from mtp_amd.awq import awq_to_gptq, load_awq_experts
+from oracle import awq_ref, gptq_ref, moe_ref
+from tests.helpers import LAYER_RTOL, bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_proj(rng, E, K, N, G):
+    q = rng.integers(0, 16, (E, K, N))
+    z = rng.integers(0, 16, (E, K // G, N))
+    s = rng.uniform(0.002, 0.02, (E, K // G, N)).astype(np.float16).astype(np.float32)
+    return q, z, s
+
+
+def _wna16(q, z, s, bf16_scales):
+    b = np.stack([awq_ref.wna16_pack(q[e]) for e in range(q.shape[0])])
+    zp = np.stack([awq_ref.wna16_zeros_pack(z[e]) for e in range(z.shape[0])])
+    st = torch.from_numpy(np.ascontiguousarray(s.transpose(0, 2, 1)))
+    st = st.to(torch.bfloat16 if bf16_scales else torch.float16)
+    return b, zp, st
+
+
+@pytest.mark.parametrize("layout,zeros,bf16", [("wna16", True, False), ("wna16", True, True),
+                                                ("wna16", False, False), ("awq", True, False)])
+def test_repack_is_bit_exact(layout, zeros, bf16):
+    rng = np.random.default_rng(7)
+    E, K, N, G = 3, 512, 256, 128
+    q, z, s = _rand_proj(rng, E, K, N, G)
+    if bf16:  # bf16-representable scales (as a bf16 checkpoint holds them)
+        s = torch.from_numpy(s).to(torch.bfloat16).float().numpy()
+    if layout == "wna16":
+        b, zp, st = _wna16(q, z, s, bf16)
+        got = awq_to_gptq(torch.from_numpy(b).cuda(), torch.from_numpy(zp).cuda() if zeros else None,
+                          st.cuda(), layout="wna16", in_features=K, group_size=G)
+        want = [awq_ref.wna16_to_gptq(b[e], zp[e] if zeros else None,
+                                      st[e].float().numpy(), G) for e in range(E)]
+    else:
+        qw = np.stack([awq_ref.awq_pack_cols(q[e]) for e in range(E)])
+        qz = np.stack([awq_ref.awq_pack_cols(z[e]) for e in range(E)])
+        sb = s.astype(np.float16).view(np.uint16)
+        got = awq_to_gptq(torch.from_numpy(qw).cuda(), torch.from_numpy(qz).cuda(),
+                          torch.from_numpy(sb.view(np.float16)).cuda(), layout="awq",
+                          in_features=K, group_size=G)
+        want = [awq_ref.awq_to_gptq(qw[e], qz[e], sb[e]) for e in range(E)]
+    torch.cuda.synchronize()
+    for e in range(E):
+        assert np.array_equal(got.qweight[e].cpu().numpy(), want[e][0])
+        assert np.array_equal(got.qzeros[e].cpu().numpy(), want[e][1])
+        assert np.array_equal(got.scales[e].cpu().view(torch.int16).numpy().view(np.uint16), want[e][2])
+    if not zeros:
+        assert bool((got.qzeros == int(np.int32(np.uint32(0x88888888).view(np.int32)))).all())
+
+
+def test_layer_on_awq_experts_matches_the_oracle():
+    """16 AWQ (wna16) experts repacked on the GPU run through the routed layer; the oracle layer
+    is computed from the oracle's own repack of the same AWQ tensors."""
+    rng = np.random.default_rng(8)
+    E, H, I, G, T, k = 16, 512, 256, 128, 6, 4
+    projs, oracle_layer = {}, {"group_size": G}
+    for name, (K, N) in (("gate_proj", (H, I)), ("up_proj", (H, I)), ("down_proj", (I, H))):
+        q, z, s = _rand_proj(rng, E, K, N, G)
+        b, zp, st = _wna16(q, z, s, False)
+        projs[name] = (torch.from_numpy(b).cuda(), torch.from_numpy(zp).cuda(), st.cuda())
+        rep = [awq_ref.wna16_to_gptq(b[e], zp[e], st[e].float().numpy(), G) for e in range(E)]
+        oracle_layer[f"{name}.qweight"] = np.stack([r[0] for r in rep])
+        oracle_layer[f"{name}.qzeros"] = np.stack([r[1] for r in rep])
+        oracle_layer[f"{name}.scales"] = np.stack([r[2] for r in rep])
+    ex = load_awq_experts(projs["gate_proj"], projs["up_proj"], projs["down_proj"], layout="wna16",
+                          hidden=H, intermediate=I, group_size=G)
+    x = synth.make_tokens(T, H, seed=81)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.1, 0.5, (T, k)).astype(np.float32)
+    for path in ("decode", "prefill"):
+        out = ops.fused_experts(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), ex,
+                                path=path)
+        torch.cuda.synchronize()
+        ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, oracle_layer)
+        err = moe_ref.rel_err(out.float().cpu().numpy(), ref)
+        print(f"  {path}: rel_err={err:.3e}", flush=True)
+        assert err <= LAYER_RTOL
+    # the dequantised weights are the AWQ formula's (q - z) * s, bit-exact in bf16
+    d = ops.dequantize(ex.down.qweight[3], ex.down.qzeros[3], ex.down.scales[3], linear_weight=False)
+    b, zp, st = (t[3].cpu().numpy() if t.dtype != torch.float16 else t[3].float().cpu().numpy()
+                 for t in projs["down_proj"])
+    want = awq_ref.wna16_dequant_f32(b, zp, st, G)
+    assert np.array_equal(bf16_bits(d), gptq_ref.f32_to_bf16_bits(want))
+
+
+def test_inexact_bf16_scale_is_refused():
+    E, K, N, G = 1, 256, 64, 128
+    b = torch.zeros(E, N, K // 2, dtype=torch.uint8, device="cuda")
+    s = torch.full((E, N, K // G), 1e-9, dtype=torch.bfloat16, device="cuda")  # fp16 underflows
+    with pytest.raises(ValueError, match="exact fp16"):
+        awq_to_gptq(b, None, s, layout="wna16", in_features=K, group_size=G)
