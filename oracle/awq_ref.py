@@ -39,7 +39,7 @@ def wna16_unpack(b: np.ndarray) -> np.ndarray:
 def wna16_pack(q: np.ndarray) -> np.ndarray:
     """q int [K, N] -> uint8 [N, K/2]."""
     q = q.astype(np.int64)
-    return ((q[0::2, :] | (q[1::2, :] << 4)).T).astype(np.uint8)
+    return np.ascontiguousarray(((q[0::2, :] | (q[1::2, :] << 4)).T).astype(np.uint8))
 
 
 def wna16_zeros_unpack(zp: np.ndarray) -> np.ndarray:
@@ -55,7 +55,7 @@ def wna16_zeros_unpack(zp: np.ndarray) -> np.ndarray:
 def wna16_zeros_pack(z: np.ndarray) -> np.ndarray:
     """z int [K/G, N] -> uint8 [N/2, K/G]."""
     z = z.astype(np.int64)
-    return ((z[:, 0::2] | (z[:, 1::2] << 4)).T).astype(np.uint8)
+    return np.ascontiguousarray(((z[:, 0::2] | (z[:, 1::2] << 4)).T).astype(np.uint8))
 
 
 def wna16_dequant_f32(b: np.ndarray, zp: np.ndarray | None, scales_f32: np.ndarray,

@@ -24,8 +24,8 @@ def _rand_proj(rng, E, K, N, G):
 
 
 def _wna16(q, z, s, bf16_scales):
-    b = np.stack([awq_ref.wna16_pack(q[e]) for e in range(q.shape[0])])
-    zp = np.stack([awq_ref.wna16_zeros_pack(z[e]) for e in range(z.shape[0])])
+    b = np.ascontiguousarray(np.stack([awq_ref.wna16_pack(q[e]) for e in range(q.shape[0])]))
+    zp = np.ascontiguousarray(np.stack([awq_ref.wna16_zeros_pack(z[e]) for e in range(z.shape[0])]))
     st = torch.from_numpy(np.ascontiguousarray(s.transpose(0, 2, 1)))
     st = st.to(torch.bfloat16 if bf16_scales else torch.float16)
     return b, zp, st
@@ -46,8 +46,8 @@ def test_repack_is_bit_exact(layout, zeros, bf16):
         want = [awq_ref.wna16_to_gptq(b[e], zp[e] if zeros else None,
                                       st[e].float().numpy(), G) for e in range(E)]
     else:
-        qw = np.stack([awq_ref.awq_pack_cols(q[e]) for e in range(E)])
-        qz = np.stack([awq_ref.awq_pack_cols(z[e]) for e in range(E)])
+        qw = np.ascontiguousarray(np.stack([awq_ref.awq_pack_cols(q[e]) for e in range(E)]))
+        qz = np.ascontiguousarray(np.stack([awq_ref.awq_pack_cols(z[e]) for e in range(E)]))
         sb = s.astype(np.float16).view(np.uint16)
         got = awq_to_gptq(torch.from_numpy(qw).cuda(), torch.from_numpy(qz).cuda(),
                           torch.from_numpy(sb.view(np.float16)).cuda(), layout="awq",
