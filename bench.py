@@ -45,8 +45,6 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=40)
     p.add_argument("--batches", default="1,8,32,64")
     p.add_argument("--prefill-tokens", type=int, default=2048)
-    p.add_argument("--decode-path", default="decode", choices=["decode", "gemv"],
-                   help="decode GEMM kernels: MFMA with in-register dequant, or VALU dot2 GEMV")
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="wall-clock budget of the CPU baseline sample (0 disables it)")
     p.add_argument("--block-batches", default="1,32",
@@ -69,11 +67,11 @@ def parse_args() -> argparse.Namespace:
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_decode_w1_bs64_hbm_traffic.md"
 
 
-def profiled_traffic(decode_path: str, batch: int) -> float | None:
+def profiled_traffic(batch: int) -> float | None:
     """HBM bytes per W1 decode launch at batch 64 from the committed rocprofv3 PMC summary
     (FETCH_SIZE and WRITE_SIZE scaled by a known-size streaming kernel); None when the run
     measures another kernel or batch, or the summary is absent."""
-    if decode_path != "decode" or batch != 64 or not TRAFFIC_PROFILE.exists():
+    if batch != 64 or not TRAFFIC_PROFILE.exists():
         return None
     for line in TRAFFIC_PROFILE.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
@@ -145,21 +143,21 @@ def main() -> int:
     keep = []
     for T in batches:
         x = synth.make_tokens(T, seed=7, device=dev)
-        need = ops.workspace_bytes(T, K, layers[0].experts, False, args.decode_path)
+        need = ops.workspace_bytes(T, K, layers[0].experts, False, "decode")
         ws = torch.zeros(need, dtype=torch.uint8, device=dev)
         outs = [torch.empty(T, H, dtype=torch.bfloat16, device=dev) for _ in range(L)]
         uniq = []
         for l, ly in enumerate(layers):
             _, ids, _ = ops.moe_layer(x, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
                                       workspace=ws, out=outs[l], return_routing=True,
-                                      path=args.decode_path)
+                                      path="decode")
             uniq.append(int(torch.unique(ids).numel()))
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for l, ly in enumerate(layers):
                 ops.moe_layer(x, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
-                              workspace=ws, out=outs[l], path=args.decode_path)
+                              workspace=ws, out=outs[l], path="decode")
         graphs[T] = g
         keep.append((x, ws, outs))
         decode[T] = {"U_per_layer_mean": sum(uniq) / L, "bytes": sum(uniq) * per_expert}
@@ -222,7 +220,7 @@ def main() -> int:
             _lib.check(lib.moe_w1_gateup_silu_v1(x.data_ptr(), Tr, K, ctypes.byref(ex), None,
                                                  s.data_ptr(), e.data_ptr(), n.data_ptr(),
                                                  ops.DECODE_BLOCK_M, e.numel(), hbuf.data_ptr(),
-                                                 ops.PATHS[args.decode_path], st))
+                                                 ops.PATHS["decode"], st))
     w1_chain()
     torch.cuda.synchronize()
     gw1 = torch.cuda.CUDAGraph()
@@ -233,11 +231,10 @@ def main() -> int:
     w1_ms = statistics.median(median_event_ms(gw1.replay, args.steps, stream))
     w1_launch_us = w1_ms * 1e3 / L
     w1_bytes_per_launch = sum(r[3] for r in routed) * w1_per_expert / L
-    traffic = profiled_traffic(args.decode_path, Tr)
+    traffic = profiled_traffic(Tr)
     roofline = {
         "bound": "hbm",
-        "kernel": ("gemm_decode_kernel<W1>" if args.decode_path == "decode" else "gemv_decode_kernel<W1>")
-                  + f" (gate_up + SiLU*mul), bs={Tr}",
+        "kernel": f"gemm_decode_kernel<W1> (gate_up + SiLU*mul), bs={Tr}",
         "achieved": w1_bytes_per_launch / (w1_launch_us * 1e-6) / 1e9,
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
@@ -391,7 +388,7 @@ def main() -> int:
             res = torch.empty_like(x0)
             h = torch.empty_like(x0)
             y = torch.empty_like(x0)
-            ws = torch.zeros(ops.workspace_bytes(T, K, layers[0].experts, False, args.decode_path),
+            ws = torch.zeros(ops.workspace_bytes(T, K, layers[0].experts, False, "decode"),
                              dtype=torch.uint8, device=dev)
 
             def chain_step(record=None):
@@ -400,11 +397,11 @@ def main() -> int:
                 for l, ly in enumerate(layers):
                     if record is None:
                         ops.moe_layer(h, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
-                                      workspace=ws, out=y, path=args.decode_path)
+                                      workspace=ws, out=y, path="decode")
                     else:
                         _, ids, _ = ops.moe_layer(h, ly.router_w, ly.experts, top_k=K,
                                                   logit_bias=ly.logit_bias, workspace=ws, out=y,
-                                                  return_routing=True, path=args.decode_path)
+                                                  return_routing=True, path="decode")
                         record.append(int(torch.unique(ids).numel()))
                     ops.rmsnorm(res, norm_w[l + 1], add=y, out=h)
 
@@ -531,7 +528,7 @@ def offload_bench(layers, args, dev) -> dict:
         pool.reset_cache()
         fresh = pool
         dec = OffloadDecoder(fresh, routers, biases, top_k=K, predictor=predictor, prefetch_k=k,
-                             path=args.decode_path)
+                             path="decode")
         step_s, base = [], None
         for t in range(n_tok):
             if t == args.offload_warmup:

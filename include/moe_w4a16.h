@@ -67,13 +67,13 @@ typedef struct moe_expert_set_v1 {
   int64_t expert_stride_bytes;
 } moe_expert_set_v1;
 
-/* Kernel path selection for the expert GEMMs (block_m: 16 for DECODE and GEMV, 128 for PREFILL).
+/* Kernel path selection for the expert GEMMs (block_m: 16 for DECODE, 128 for PREFILL).
  *   DECODE : MFMA 16x16x32 bf16 on 16-slot blocks, int4 dequantised in registers into the
  *            MFMA operand, K split across waves (token batches up to a few hundred slots);
  *   PREFILL: MFMA on 128-slot blocks with dequantised int4 tiles staged in LDS;
- *   GEMV   : VALU v_dot2_f32_bf16 per token with shuffle K-reduction (kept for comparison);
- *   AUTO   : PREFILL when T * top_k >= 1024, else DECODE. */
-enum { MOE_PATH_AUTO = 0, MOE_PATH_DECODE = 1, MOE_PATH_PREFILL = 2, MOE_PATH_GEMV = 3 };
+ *   AUTO   : PREFILL when T * top_k >= 1024, else DECODE.
+ * Any other value is refused with MOE_ERR_UNSUPPORTED (the workspace query returns -1). */
+enum { MOE_PATH_AUTO = 0, MOE_PATH_DECODE = 1, MOE_PATH_PREFILL = 2 };
 
 int moe_w4a16_abi_version(void);
 const char* moe_w4a16_last_error(void);

@@ -28,7 +28,6 @@ MOE_ERR_HIP = 200
 PATH_AUTO = 0
 PATH_DECODE = 1
 PATH_PREFILL = 2
-PATH_GEMV = 3
 
 EXPORTED = (
     "moe_w4a16_abi_version",

@@ -86,8 +86,10 @@ ExpertsDev make_experts_dev(const moe_expert_set_v1* ex, const moe_expert_set_v1
   return d;
 }
 
+// The path the kernels run (AUTO resolved from the slot count); -1 for an unknown value.
 int resolve_path(int path, int T, int top_k) {
-  if (path == MOE_PATH_DECODE || path == MOE_PATH_PREFILL || path == MOE_PATH_GEMV) return path;
+  if (path == MOE_PATH_DECODE || path == MOE_PATH_PREFILL) return path;
+  if (path != MOE_PATH_AUTO) return -1;
   return (T * top_k >= 1024) ? MOE_PATH_PREFILL : MOE_PATH_DECODE;
 }
 
@@ -98,7 +100,6 @@ hipError_t dispatch_w1(int path, const uint16_t* x, const ExpertsDev& ed, const 
                        const int32_t* border, int bm, int cap, uint16_t* h, hipStream_t s) {
   if (path == MOE_PATH_PREFILL)
     return launch_w1_prefill(x, ed, sd, sorted, eids, ntpp, border, bm, cap, h, s);
-  if (path == MOE_PATH_GEMV) return launch_w1_decode(x, ed, sd, sorted, eids, ntpp, bm, cap, h, s);
   return launch_w1_decode_mfma(x, ed, sd, sorted, eids, ntpp, cap, h, s);
 }
 
@@ -108,7 +109,6 @@ hipError_t dispatch_w2(int path, const uint16_t* h, const ExpertsDev& ed, const 
                        hipStream_t s) {
   if (path == MOE_PATH_PREFILL)
     return launch_w2_prefill(h, ed, sd, sorted, eids, ntpp, border, bm, cap, w, ys, s);
-  if (path == MOE_PATH_GEMV) return launch_w2_decode(h, ed, sd, sorted, eids, ntpp, bm, cap, w, ys, s);
   return launch_w2_decode_mfma(h, ed, sd, sorted, eids, ntpp, cap, w, ys, s);
 }
 
@@ -361,7 +361,9 @@ int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
   if (T < 0 || top_k < 1) return fail(MOE_ERR_SHAPE, "w1: T=%d top_k=%d", T, top_k);
   if (T == 0) return MOE_OK;
   if (!x || !sorted_ids || !expert_ids || !ntpp || !h) return fail(MOE_ERR_NULL, "w1: NULL pointer");
+  const int path_in = path;
   path = resolve_path(path, T, top_k);
+  if (path < 0) return fail(MOE_ERR_UNSUPPORTED, "w1: unknown path %d", path_in);
   if (block_m != block_m_of(path))
     return fail(MOE_ERR_UNSUPPORTED, "w1: block_m=%d, path %d needs %d", block_m, path,
                 block_m_of(path));
@@ -383,7 +385,9 @@ int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
   if (T == 0) return MOE_OK;
   if (!h || !sorted_ids || !expert_ids || !ntpp || !topk_weights || !ys)
     return fail(MOE_ERR_NULL, "w2: NULL pointer");
+  const int path_in = path;
   path = resolve_path(path, T, top_k);
+  if (path < 0) return fail(MOE_ERR_UNSUPPORTED, "w2: unknown path %d", path_in);
   if (block_m != block_m_of(path))
     return fail(MOE_ERR_UNSUPPORTED, "w2: block_m=%d, path %d needs %d", block_m, path,
                 block_m_of(path));
@@ -426,6 +430,7 @@ int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_
                                      int32_t has_shared, int32_t path) {
   if (!experts || T < 0 || top_k < 1) return -1;
   path = resolve_path(path, T, top_k);
+  if (path < 0) return -1;
   return (int64_t)layout(T, top_k, experts, has_shared ? 1 : 0, path).total;
 }
 
@@ -443,7 +448,9 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   const int E = experts->num_experts;
   if (top_k < 1 || top_k > E || top_k > 64)
     return fail(MOE_ERR_SHAPE, "layer: top_k=%d outside [1, min(num_experts, 64)]", top_k);
+  const int path_in = path;
   path = resolve_path(path, T, top_k);
+  if (path < 0) return fail(MOE_ERR_UNSUPPORTED, "layer: unknown path %d", path_in);
   const Workspace L = layout(T, top_k, experts, shared ? 1 : 0, path);
   if (workspace_bytes < (int64_t)L.total)
     return fail(MOE_ERR_WORKSPACE, "layer: workspace %lld < required %lld",
@@ -502,7 +509,9 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
   if (!x || !topk_ids || !topk_weights || !out || !workspace)
     return fail(MOE_ERR_NULL, "experts: NULL pointer");
   if (shared && !shared_gate_w) return fail(MOE_ERR_NULL, "experts: shared expert needs shared_gate_w");
+  const int path_in = path;
   path = resolve_path(path, T, top_k);
+  if (path < 0) return fail(MOE_ERR_UNSUPPORTED, "experts: unknown path %d", path_in);
   const Workspace L = layout(T, top_k, experts, shared ? 1 : 0, path);
   if (workspace_bytes < (int64_t)L.total)
     return fail(MOE_ERR_WORKSPACE, "experts: workspace %lld < required %lld",

@@ -87,13 +87,6 @@ hipError_t launch_w1_decode_slotgrid(const uint16_t* x, const ExpertsDev& ed, co
 hipError_t launch_w2_decode_slotgrid(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                      const SlotGrid& sg, float* ys, hipStream_t stream);
 
-// Decode path on VALU dot products (v_dot2_f32_bf16) with shuffle K-reduction.
-hipError_t launch_w1_decode(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
-                            const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                            int BM, int cap, uint16_t* h, hipStream_t stream);
-hipError_t launch_w2_decode(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
-                            const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
-                            int BM, int cap, const float* topk_w, float* ys, hipStream_t stream);
 // ids == nullptr: every slot is summed; otherwise routed slots with a dropped expert are skipped.
 hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared,
                           const int32_t* ids, int num_experts, const int32_t* expert_row,

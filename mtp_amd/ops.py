@@ -14,8 +14,7 @@ import torch
 from mtp_amd import _lib
 from mtp_amd.weights import MoeExperts
 
-PATHS = {"auto": _lib.PATH_AUTO, "decode": _lib.PATH_DECODE, "prefill": _lib.PATH_PREFILL,
-         "gemv": _lib.PATH_GEMV}
+PATHS = {"auto": _lib.PATH_AUTO, "decode": _lib.PATH_DECODE, "prefill": _lib.PATH_PREFILL}
 DECODE_BLOCK_M = 16
 PREFILL_BLOCK_M = 128
 OUT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -63,6 +63,22 @@ def test_workspace_too_small_is_rejected():
     assert rc == _lib.MOE_ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("path", [3, -1, 99])
+def test_unknown_path_is_refused(path):
+    """Only AUTO, DECODE and PREFILL exist; any other path value is an error, never AUTO."""
+    lib = _lib.load()
+    ex = _fake_set()
+    assert lib.moe_layer_workspace_bytes_v1(16, 8, ctypes.byref(ex), 0, path) == -1
+    need = lib.moe_layer_workspace_bytes_v1(16, 8, ctypes.byref(ex), 0, 0)
+    rc = lib.moe_layer_v1(0x10, 16, 0x10, None, 8, ctypes.byref(ex), None, None, 0x10, need,
+                          0x10, None, None, path, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED
+    assert f"unknown path {path}".encode() in lib.moe_w4a16_last_error()
+    rc = lib.moe_w1_gateup_silu_v1(0x10, 4, 8, ctypes.byref(ex), None, 0x10, 0x10, 0x10, 16, 1,
+                                   0x10, path, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize("T,k,E,shared,BM", [(1, 8, 256, 0, 16), (64, 8, 256, 1, 16),
                                                (2048, 8, 256, 0, 128), (3, 4, 16, 1, 4)])
 def test_capacity_blocks_matches_oracle_bound(T, k, E, shared, BM):

@@ -44,7 +44,7 @@ def _check_layer(layer_cpu, T, top_k, path, seed=7):
 
 
 @pytest.mark.parametrize("T", [1, 3, 16, 40])
-@pytest.mark.parametrize("path", ["decode", "prefill", "gemv"])
+@pytest.mark.parametrize("path", ["decode", "prefill"])
 def test_small_layer(T, path):
     _say(f"small layer T={T} path={path}")
     _check_layer(small_layer(0), T, 4, path)
@@ -58,8 +58,8 @@ def test_token_sum_w2_with_shared_expert(T):
     _check_layer(small_layer(2, shared=True), T, 4, "decode")
 
 
-@pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode"), (16, "gemv"),
-                                    (32, "decode"), (64, "decode")])
+@pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode"), (32, "decode"),
+                                    (64, "decode")])
 def test_config1_full_shape(T, path):
     """Config 1: hidden 2048, 256 experts, intermediate 512, top-8, 16 tokens."""
     _say(f"config1 T={T} path={path}")
@@ -92,7 +92,7 @@ def test_decode_and_prefill_paths_agree_on_zipf_batch():
     layer = to_gpu(synth.make_layer(2, zipf=True))
     x = synth.make_tokens(64, seed=11).cuda()
     outs = [ops.moe_layer(x, layer.router_w, layer.experts, logit_bias=layer.logit_bias, path=p)
-            for p in ("decode", "prefill", "gemv")]
+            for p in ("decode", "prefill")]
     for o in outs[1:]:
         assert moe_ref.rel_err(o.float().cpu().numpy(), outs[0].float().cpu().numpy()) < 1e-2
 
@@ -137,7 +137,7 @@ def test_expert_row_indirection_matches_direct():
                         expert_row=inv.to(torch.int32).cuda(), num_experts=E)
     for T in (6, 9):  # 6: W2 sums the token's rows itself; 9: blocked W2 + moe_sum
         x = synth.make_tokens(T, 512, seed=4).cuda()
-        for path in ("decode", "prefill", "gemv"):
+        for path in ("decode", "prefill"):
             a = ops.moe_layer(x, layer.router_w, layer.experts, top_k=4, path=path)
             b = ops.moe_layer(x, layer.router_w, pooled, top_k=4, path=path)
             assert torch.equal(a, b)
@@ -173,8 +173,8 @@ def test_layer_is_deterministic():
     assert all(torch.equal(outs[0], o) for o in outs[1:])
 
 
-@pytest.mark.parametrize("path,T", [("decode", 1), ("decode", 2), ("decode", 5), ("gemv", 5),
-                                    ("prefill", 64), ("decode", 64)])
+@pytest.mark.parametrize("path,T", [("decode", 1), ("decode", 2), ("decode", 5), ("prefill", 64),
+                                    ("decode", 64)])
 def test_dropped_slots_contribute_zero(path, T):
     """Ids outside [0, E) are dropped (reference: vllm_router_trace.py:14138-14153); the other
     slots of the token still count, on every path including the fused W2 + sum."""
@@ -212,7 +212,7 @@ def test_decode_repeated_ids(case):
     w = rng.uniform(0.05, 0.3, size=(T, k)).astype(np.float32)
     x = synth.make_tokens(T, 512, seed=56)
     ref = moe_ref.moe_layer_f32(bf16_bits(x), ids, w, experts_to_np(lay.experts))
-    for path in ("decode", "prefill", "gemv"):
+    for path in ("decode", "prefill"):
         got = ops.fused_experts(x.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
                                 g.experts, path=path)
         torch.cuda.synchronize()

@@ -46,7 +46,7 @@ def _slot_bytes_ok(pool: OffloadedExperts, layer: int, experts, blobs: torch.Ten
         assert torch.equal(pool.device_pool[layer, s], blobs[e]), (layer, e, s)
 
 
-@pytest.mark.parametrize("path", ["decode", "gemv", "prefill"])
+@pytest.mark.parametrize("path", ["decode", "prefill"])
 def test_pooled_layer_matches_resident(pooled, path):
     layers, pool = pooled
     rng = np.random.default_rng(11)
@@ -120,7 +120,7 @@ def test_predictor_rejects_bad_shapes():
         ops.predictor_topk(h, w1, w2, 4)
 
 
-@pytest.mark.parametrize("path", ["decode", "gemv", "prefill"])
+@pytest.mark.parametrize("path", ["decode", "prefill"])
 def test_nonresident_expert_is_dropped(pooled, path):
     """A pool view maps experts that are not resident to row -1: their slots contribute zero
     (never a read through a negative row)."""
