@@ -136,7 +136,11 @@ Workspace layout(int T, int top_k, const moe_expert_set_v1* ex, int has_shared, 
   L.ntpp = o;   o += 256;
   L.border = o; o += align256((size_t)L.cap * 4);  // block order of the large-input align
   L.h = o;      o += align256(slots * I * 2);
-  L.ys = o;     o += align256(slots * H * 4);
+  // ys: fp32 slot rows, or at one or two decode tokens the fused W1+W2 partial rows
+  size_t ys_bytes = slots * H * 4;
+  if (path == MOE_PATH_DECODE && T <= kGridTopkMaxTokens)
+    ys_bytes = std::max(ys_bytes, slots * (size_t)(I / 32) * H * 4);
+  L.ys = o;     o += align256(ys_bytes);
   L.total = o;
   return L;
 }
@@ -174,6 +178,16 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   const bool grid = routing == ROUTE_GRID_LOGITS || routing == ROUTE_GRID_IDS;
   if (grid) {
     const SlotGrid sg{1, routing == ROUTE_GRID_LOGITS ? at<float>(ws, L.logits) : nullptr, ids, w};
+    const int nct = ex->intermediate / 32;
+    if (T <= kGridTopkMaxTokens && w1w2_fused_fits(ed, sd) &&
+        partial_sum_fits(top_k, has_shared, ex->hidden, nct)) {
+      // one or two tokens: W2 runs inside the W1 workgroups (weighted partial rows per W1
+      // column block), then one fixed-order sum per token
+      MOE_CHECK_HIP(launch_w1w2_slotgrid(x, ed, sd, sg, ys, stream), "w1 + w2 (slot grid)");
+      MOE_CHECK_HIP(launch_partial_sum(ys, T, top_k, ex->hidden, nct, has_shared, out, stream),
+                    "partial sum");
+      return MOE_OK;
+    }
     MOE_CHECK_HIP(launch_w1_decode_slotgrid(x, ed, sd, sg, h, stream), "w1 (slot grid)");
   } else {
     if (routing == ROUTE_ALIGN) {

@@ -41,6 +41,7 @@ namespace {
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 
 constexpr int kBM = kDecodeBlockM;  // 16 slots
+constexpr int kW2Groups = 4;        // fused W2: 64-column groups of the output per wave
 constexpr uint32_t kOnes = 0x3F803F80u;
 
 enum { DEC_W1 = 1, DEC_W2 = 2 };
@@ -277,7 +278,12 @@ MOE_DEV void projections(const ExpertsDev& ed, int mode, bool is_shared, ProjDev
 // NB > 0 and NGW == 0: runtime loop over the wave's groups with an NB-deep ring; NB < 0: a
 // slice of exactly -NB groups, all loaded up front; NGW > 0: a slice of exactly NGW groups with
 // an NB-deep ring, unrolled.
-template <int MODE, int SPG, int KS, int CT, int NB, int NGW = 0>
+// FW2 (W1 on the slot grid, CT == 2): W2 fused in. The block's 32 h columns are the K rows
+// [32 x, 32 x + 32) of the down projection (inside one quantisation group); after the W1
+// epilogue every wave multiplies the block's h rows (from LDS) by its kW2Groups x 64 output
+// columns and writes the weighted fp32 partial rows ys[slot][x][n] (partial_sum adds them).
+// The workgroup of a dropped expert writes zero rows, so every partial row is written.
+template <int MODE, int SPG, int KS, int CT, int NB, int NGW = 0, bool FW2 = false>
 __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
     const uint16_t* __restrict__ act, ExpertsDev ed, SlotsDev sd,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ eids,
@@ -286,15 +292,16 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
   constexpr int NP = (MODE == DEC_W1) ? 2 : 1;  // projections (gate, up) or (down)
   constexpr int NT = NP * CT;                    // MFMA N-subtiles per lane
   constexpr int TW = 16 * CT;                    // columns per block
+  static_assert(!FW2 || (MODE == DEC_W1 && CT == 2), "fused W2: W1 blocks of 32 columns");
   __shared__ float red[(KS > 1 ? KS - 1 : 1) * NT * 4 * 64];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar K-slice offsets
   int e, f_m, f_out[4];  // expert; A row of this lane; D rows of this lane
+  __shared__ float s_w[kSlotGridMaxSlots + kTopkAlignMaxTokens];  // slot grid: routed weights
   if (sg.active) {
     // Slot grid (SlotGrid in launch.h): slots from the routed ids, no align pass.
     __shared__ int s_ids[kSlotGridMaxSlots];
-    __shared__ float s_w[kSlotGridMaxSlots + kTopkAlignMaxTokens];
     __shared__ int s_rows[kBM];
     const int E = ed.num_experts, routed = sd.T * sd.top_k, n_slots = sd.num_slots;
     if (sg.logits) {  // every workgroup computes the same top-k of the (at most 8) tokens
@@ -306,8 +313,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
         topk_token_lds_any(row, E, sd.top_k, lane, s_ids + t * sd.top_k, s_w + t * sd.top_k);
         if (shared && lane == 0) s_w[routed + t] = 1.0f / (1.0f + expf(-g));
       }
-    } else if (tid < routed) {
-      s_ids[tid] = sg.ids[tid];
+    } else {
+      if (tid < routed) s_ids[tid] = sg.ids[tid];
+      if (FW2 && tid < n_slots) s_w[tid] = sg.weights[tid];
     }
     __syncthreads();
     if (sg.logits && blockIdx.x == 0 && blockIdx.y == 0) {  // publish for W2 and the caller
@@ -319,7 +327,11 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
     e = expert_of(b);
     const uint64_t mask = __ballot(lane < n_slots && expert_of(lane) == e);
     const int rank_b = __popcll(mask & ((1ull << b) - 1));  // occurrences of e before slot b
-    if (rank_b % kBM != 0 || !expert_ok(ed, e)) return;   // uniform over the workgroup
+    if constexpr (!FW2) {
+      if (rank_b % kBM != 0 || !expert_ok(ed, e)) return;  // uniform over the workgroup
+    } else {
+      if (rank_b % kBM != 0) return;  // a dropped expert still writes its (zero) partial rows
+    }
     const int rank = __popcll(mask & ((1ull << lane) - 1));
     if (wave == 0 && ((mask >> lane) & 1) && rank >= rank_b && rank < rank_b + kBM)
       s_rows[rank - rank_b] = lane;
@@ -330,6 +342,15 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
     for (int el = 0; el < 4; ++el) {
       const int r = 4 * (lane >> 4) + el;
       f_out[el] = r < cnt ? s_rows[r] : n_slots;
+    }
+    if constexpr (FW2) {
+      if (!expert_ok(ed, e)) {  // dropped slots: zero partial rows for this column block
+        const int H = ed.hidden, q4 = H / 4;
+        for (int i = tid; i < cnt * q4; i += blockDim.x)
+          *reinterpret_cast<float4*>(ys + ((int64_t)s_rows[i / q4] * gridDim.x + blockIdx.x) * H +
+                                     4 * (i % q4)) = float4{0.f, 0.f, 0.f, 0.f};
+        return;
+      }
     }
   } else {
     // Block metadata: every load below is in bounds for any b < gridDim.y, so all of them are
@@ -365,6 +386,32 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
   const int cl = blockIdx.x * TW + CT * m;  // this lane's first column
   const DecodeTile<NP, SPG, CT> tile(pj, av, NOUT, G, kw0, kslice, cl, kq);
 
+  // FW2: the down projection's words, scales and zeros for this wave's output columns, loaded
+  // with the W1 stream. Lane (c = lane & 15, kq) takes packed row x * 4 + kq (TW == 32) and the
+  // 4 columns n0 + 4 c .. + 3 of each 64-column group: word t is the B fragment of MFMA tile t.
+  [[maybe_unused]] u32x4 w2q[FW2 ? kW2Groups : 1];
+  [[maybe_unused]] u32x2 w2s[FW2 ? kW2Groups : 1];
+  [[maybe_unused]] uint32_t w2z[FW2 ? kW2Groups : 1];
+  [[maybe_unused]] int w2n0 = 0;
+  if constexpr (FW2) {
+    const int I = ed.inter, H = ed.hidden;
+    ProjDev pd[1];
+    projections(ed, DEC_W2, is_shared, pd);
+    pd[0] = proj_row(pd[0], is_shared ? 0 : ed.row_stride, row, I / 8, I / G, H);
+    const int k0 = blockIdx.x * TW, g2 = k0 / G;
+    w2n0 = wave * (kW2Groups * 64) + 4 * m;
+    const __amdgpu_buffer_rsrc_t q2 = buf_rsrc(pd[0].qweight), s2 = buf_rsrc(pd[0].scales),
+                                 z2 = buf_rsrc(pd[0].qzeros);
+#pragma unroll
+    for (int gi = 0; gi < kW2Groups; ++gi) {
+      const uint32_t n = (uint32_t)(w2n0 + 64 * gi);
+      w2q[gi] = buf_ld128<kBufNontemporal>(q2, ((uint32_t)(k0 / 8 + kq) * (uint32_t)H + n) * 4u);
+      w2s[gi] = buf_ld64(s2, ((uint32_t)g2 * (uint32_t)H + n) * 2u);
+      w2z[gi] = buf_ld32(z2, ((uint32_t)g2 * (uint32_t)(H / 8) + (n >> 3)) * 4u);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // issued here, with the W1 stream, not at their use
+  }
+
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -384,12 +431,75 @@ __global__ __launch_bounds__(64 * KS) void gemm_decode_kernel(
         for (int i = 0; i < 4; ++i) red[(((wave - 1) * NT + t) * 4 + i) * 64 + lane] = acc[t][i];
     }
     __syncthreads();
-    if (wave != 0) return;
-    for (int w = 1; w < KS; ++w)
+    if constexpr (!FW2) {
+      if (wave != 0) return;
+      for (int w = 1; w < KS; ++w)
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] += red[(((w - 1) * NT + t) * 4 + i) * 64 + lane];
+          for (int i = 0; i < 4; ++i) acc[t][i] += red[(((w - 1) * NT + t) * 4 + i) * 64 + lane];
+    } else if (wave == 0) {
+      for (int w = 1; w < KS; ++w)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][i] += red[(((w - 1) * NT + t) * 4 + i) * 64 + lane];
+    }
+  }
+
+  if constexpr (FW2) {
+    // h rows of the block (bf16, as W1 writes them) into LDS as [16 rows][16 column pairs]
+    __shared__ uint32_t s_h[kBM * 16];
+    if (wave == 0) {
+#pragma unroll
+      for (int el = 0; el < 4; ++el) {
+        const bool real = (unsigned)f_out[el] < (unsigned)sd.num_slots;
+        s_h[(4 * kq + el) * 16 + m] =
+            real ? pack_bf16x2(silu_f32(acc[0][el]) * acc[CT][el],
+                               silu_f32(acc[1][el]) * acc[CT + 1][el])
+                 : 0u;
+      }
+    }
+    __syncthreads();
+    // A: row m, k 8 kq .. 8 kq + 7 of the block's 32 h columns; X[row] = sum of the row's h
+    const u32x4 hv = {s_h[m * 16 + 4 * kq], s_h[m * 16 + 4 * kq + 1], s_h[m * 16 + 4 * kq + 2],
+                      s_h[m * 16 + 4 * kq + 3]};
+    const bf16x8_v av2 = act_frag(hv);
+    const f32x4 tx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        av2, as_frag(kOnes, kOnes, kOnes, kOnes), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const int H = ed.hidden, nct = gridDim.x;
+    float wrow[4];
+#pragma unroll
+    for (int el = 0; el < 4; ++el)
+      wrow[el] = (unsigned)f_out[el] < (unsigned)sd.num_slots ? s_w[f_out[el]] : 0.0f;
+#pragma unroll
+    for (int gi = 0; gi < kW2Groups; ++gi) {
+      f32x4 d[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av2, weight_frag(w2q[gi][t]),
+                                                       f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      const int n = w2n0 + 64 * gi;
+      float sc[4], zb[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        sc[t] = f16_to_f32(t & 2 ? ((t & 1) ? (w2s[gi][1] >> 16) : (w2s[gi][1] & 0xFFFFu))
+                                 : ((t & 1) ? (w2s[gi][0] >> 16) : (w2s[gi][0] & 0xFFFFu)));
+        zb[t] = kMagicBias + (float)((w2z[gi] >> (4 * ((n & 7) + t))) & 0xFu);
+      }
+#pragma unroll
+      for (int el = 0; el < 4; ++el) {
+        const int f = f_out[el];
+        if ((unsigned)f >= (unsigned)sd.num_slots) continue;
+        float4 v;
+        v.x = wrow[el] * (sc[0] * __builtin_fmaf(-zb[0], tx[el], d[0][el]));
+        v.y = wrow[el] * (sc[1] * __builtin_fmaf(-zb[1], tx[el], d[1][el]));
+        v.z = wrow[el] * (sc[2] * __builtin_fmaf(-zb[2], tx[el], d[2][el]));
+        v.w = wrow[el] * (sc[3] * __builtin_fmaf(-zb[3], tx[el], d[3][el]));
+        *reinterpret_cast<float4*>(ys + ((int64_t)f * nct + blockIdx.x) * H + n) = v;
+      }
+    }
+    return;
   }
 
   // D[i][j] of a 16x16 tile: lane j + 16*(i/4), element i%4 -> row 4*(lane>>4)+el; N-subtile t
@@ -653,6 +763,33 @@ hipError_t launch_w2_decode_slotgrid(const uint16_t* h, const ExpertsDev& ed, co
     return hipErrorInvalidValue;
   return launch_decode_picked<DEC_W2>(h, ed, sd, nullptr, nullptr, nullptr, 0, sg.weights, nullptr,
                                       ys, sg, stream);
+}
+
+// W1 + fused W2 partials on the slot grid: group 128, one wave per two groups of K = hidden
+// (all loads up front), and hidden = 4 x 64 output columns per wave.
+bool w1w2_fused_fits(const ExpertsDev& ed, const SlotsDev& sd) {
+  const int H = ed.hidden, ks = H / 256;
+  return ed.group == 128 && H % 256 == 0 && (ks == 2 || ks == 4 || ks == 8) &&
+         ed.inter % 32 == 0 && decode_offsets_fit(ed, sd) &&
+         slot_grid_fits(sd.T, sd.top_k, sd.num_slots > sd.T * sd.top_k ? 1 : 0) &&
+         (int64_t)sd.num_slots * (ed.inter / 32) * H * 4 < kOutOfRange;
+}
+
+hipError_t launch_w1w2_slotgrid(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                                const SlotGrid& sg, float* part, hipStream_t stream) {
+  if (!sg.active || !w1w2_fused_fits(ed, sd)) return hipErrorInvalidValue;
+  const dim3 grid(ed.inter / 32, sd.num_slots);
+  switch (ed.hidden / 256) {
+#define MOE_W1W2(KSV)                                                                          \
+  case KSV:                                                                                    \
+    hipLaunchKernelGGL((gemm_decode_kernel<DEC_W1, 4, KSV, 2, -2, 0, true>), grid,             \
+                       dim3(64 * KSV), 0, stream, x, ed, sd, nullptr, nullptr, nullptr,        \
+                       nullptr, nullptr, part, sg);                                            \
+    return hipGetLastError();
+    MOE_W1W2(2) MOE_W1W2(4) MOE_W1W2(8)
+#undef MOE_W1W2
+    default: return hipErrorInvalidValue;
+  }
 }
 
 bool w2_token_sum_fits(const ExpertsDev& ed, const SlotsDev& sd) {

@@ -106,6 +106,14 @@ constexpr int kTokenSumMaxTokens = 8;
 constexpr int kGridTopkMaxTokens = 2;
 constexpr int kTokenSumMaxWaves = 9;  // top_k <= 8 plus the shared expert
 bool w2_token_sum_fits(const ExpertsDev& ed, const SlotsDev& sd);
+// W1 with W2 fused in, on the slot grid (T <= kGridTopkMaxTokens): part = fp32 partial rows
+// [num_slots][inter / 32][hidden] (weighted), summed per token by launch_partial_sum.
+bool w1w2_fused_fits(const ExpertsDev& ed, const SlotsDev& sd);
+hipError_t launch_w1w2_slotgrid(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
+                                const SlotGrid& sg, float* part, hipStream_t stream);
+bool partial_sum_fits(int top_k, int has_shared, int H, int nct);
+hipError_t launch_partial_sum(const float* part, int T, int top_k, int H, int nct, int has_shared,
+                              uint16_t* out, hipStream_t stream);
 hipError_t launch_w2_token_sum(const uint16_t* h, const ExpertsDev& ed, const SlotsDev& sd,
                                const int32_t* ids, const float* topk_w, uint16_t* out,
                                hipStream_t stream);

@@ -148,7 +148,73 @@ hipError_t launch_moe_sum_t(const YT* ys, int T, int top_k, int H, int has_share
                                      out, stream);
 }
 
+// Sum of the fused W1+W2 partial rows (gemm_decode_kernel FW2): out[t][n] = bf16 of the fp32
+// sum over the token's contributing slots (routed t*top_k .. t*top_k + top_k - 1, then the
+// shared slot T*top_k + t) and over the nct column tiles c of part[slot][c][n], in that
+// (slot, c) order split into 16 consecutive runs whose sums are added in run order. A block
+// covers 64 columns of one token: thread (run = tid >> 4, column quad tid & 15). Every partial
+// row is written (zeros for a dropped expert), so no ids are read.
+constexpr int kPartialRuns = 16;
+constexpr int kPartialMaxPerRun = 16;  // slots x column tiles <= 256
+__global__ __launch_bounds__(256) void partial_sum_kernel(
+    const float* __restrict__ part, int T, int top_k, int H, int nct, int has_shared,
+    uint16_t* __restrict__ out) {
+  __shared__ float4 s_run[kPartialRuns][16];
+  const int t = blockIdx.y, tid = threadIdx.x, cq = tid & 15, run = tid >> 4;
+  const int n = blockIdx.x * 64 + 4 * cq;
+  const int S = top_k + has_shared, npair = S * nct;
+  const int per = (npair + kPartialRuns - 1) / kPartialRuns;
+  const int routed = T * top_k, n_slots = routed + (has_shared ? T : 0);
+  const __amdgpu_buffer_rsrc_t pr =
+      buf_rsrc(part, (uint32_t)n_slots * (uint32_t)nct * (uint32_t)H * 4u);
+  u32x4 v[kPartialMaxPerRun];
+#pragma unroll
+  for (int q = 0; q < kPartialMaxPerRun; ++q) {
+    const int p = run * per + q;
+    const bool in = q < per && p < npair;
+    const int si = in ? p / nct : 0, c = in ? p - si * nct : 0;
+    const int f = si < top_k ? t * top_k + si : routed + t;
+    v[q] = buf_ld128(pr, in ? (((uint32_t)f * (uint32_t)nct + (uint32_t)c) * (uint32_t)H +
+                               (uint32_t)n) * 4u
+                            : kOutOfRange);
+  }
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < kPartialMaxPerRun; ++q) {
+    acc.x += __uint_as_float(v[q][0]);
+    acc.y += __uint_as_float(v[q][1]);
+    acc.z += __uint_as_float(v[q][2]);
+    acc.w += __uint_as_float(v[q][3]);
+  }
+  s_run[run][cq] = acc;
+  __syncthreads();
+  if (run != 0) return;
+#pragma unroll
+  for (int r = 1; r < kPartialRuns; ++r) {
+    const float4 o = s_run[r][cq];
+    acc.x += o.x;
+    acc.y += o.y;
+    acc.z += o.z;
+    acc.w += o.w;
+  }
+  *reinterpret_cast<u32x2*>(out + (int64_t)t * H + n) =
+      u32x2{pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w)};
+}
+
 }  // namespace
+
+bool partial_sum_fits(int top_k, int has_shared, int H, int nct) {
+  return H % 64 == 0 && (top_k + has_shared) * nct <= kPartialRuns * kPartialMaxPerRun;
+}
+
+hipError_t launch_partial_sum(const float* part, int T, int top_k, int H, int nct, int has_shared,
+                              uint16_t* out, hipStream_t stream) {
+  if (!partial_sum_fits(top_k, has_shared, H, nct)) return hipErrorInvalidValue;
+  if (T == 0) return hipSuccess;
+  hipLaunchKernelGGL(partial_sum_kernel, dim3(H / 64, T), dim3(256), 0, stream, part, T, top_k, H,
+                     nct, has_shared, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_moe_sum(const float* ys, int T, int top_k, int H, int has_shared,
                           const int32_t* ids, int num_experts, const int32_t* expert_row,
