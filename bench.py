@@ -375,9 +375,12 @@ def main() -> int:
         del shared, sgate
 
     # ------------------------------------- decode chain: the layers in a decode loop (dependent)
-    # Per layer l: y = MoE_l(h); res = res + y; h = RMSNorm_{l+1}(res) (the decoder loop around
-    # moe_forward_with_trace with mtp_rms_norm), so every layer's routing depends on the previous
-    # layer's output. Same layers, weights and routing bias as the sweep.
+    # Per layer l: res = res + y_{l-1}; h = RMSNorm_l(res); y_l = MoE_l(h) (the decoder loop around
+    # moe_forward_with_trace with mtp_rms_norm), then the final RMSNorm_L, so every layer's routing
+    # depends on the previous layer's output. Each step of the timed loop is one
+    # moe_norm_layer_v1 call (the router normalises its own tokens) on two alternating residual
+    # buffers; the bits equal the rmsnorm + moe_layer loop, which records the routing. Same
+    # layers, weights and routing bias as the sweep.
     chain = {}
     chain_batches = [int(b) for b in args.chain_batches.split(",") if b]
     if chain_batches:
@@ -391,22 +394,31 @@ def main() -> int:
             ws = torch.zeros(ops.workspace_bytes(T, K, layers[0].experts, False, "decode"),
                              dtype=torch.uint8, device=dev)
 
-            def chain_step(record=None):
+            res2 = torch.empty_like(x0)
+
+            def record_routing(record):
                 res.copy_(x0)
                 ops.rmsnorm(res, norm_w[0], out=h)
                 for l, ly in enumerate(layers):
-                    if record is None:
-                        ops.moe_layer(h, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
-                                      workspace=ws, out=y, path="decode")
-                    else:
-                        _, ids, _ = ops.moe_layer(h, ly.router_w, ly.experts, top_k=K,
-                                                  logit_bias=ly.logit_bias, workspace=ws, out=y,
-                                                  return_routing=True, path="decode")
-                        record.append(int(torch.unique(ids).numel()))
+                    _, ids, _ = ops.moe_layer(h, ly.router_w, ly.experts, top_k=K,
+                                              logit_bias=ly.logit_bias, workspace=ws, out=y,
+                                              return_routing=True, path="decode")
+                    record.append(int(torch.unique(ids).numel()))
                     ops.rmsnorm(res, norm_w[l + 1], add=y, out=h)
 
+            def chain_step():
+                bufs = (res, res2)
+                res.copy_(x0)
+                cur = 0
+                for l, ly in enumerate(layers):
+                    ops.norm_layer(bufs[cur], ly.router_w, ly.experts, norm_w[l],
+                                   add=y if l else None, res_out=bufs[1 - cur], x_out=h, top_k=K,
+                                   logit_bias=ly.logit_bias, workspace=ws, out=y, path="decode")
+                    cur = 1 - cur
+                ops.rmsnorm(bufs[cur], norm_w[L], add=y, out=h)
+
             uniq = []
-            chain_step(uniq)
+            record_routing(uniq)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):

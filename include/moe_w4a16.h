@@ -175,6 +175,25 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
                  uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
                  void* stream);
 
+/* A decoder step's residual add + RMSNorm in front of the routed layer, as the decoder loop runs
+ * them (mtp_rms_norm, src/mtp_expert_prefetch/mtp/extra_tensors.py:40-48, before
+ * moe_forward_with_trace in the layer loop of
+ * src/mtp_expert_prefetch/tracing/vllm_router_trace.py:17895-17965):
+ *   res_out = bf16(res_in + add)   (add NULL: res_out = res_in)
+ *   x_out   = the moe_rmsnorm_v1 output of res_out with norm_w, eps
+ *   out     = moe_layer_v1(x_out, ...)
+ * The bits equal moe_rmsnorm_v1 followed by moe_layer_v1. On the decode path with T <= 64,
+ * hidden <= 2048 and res_out != res_in the router normalises its own tokens (no separate norm
+ * launch); otherwise the norm runs first. res_out may equal res_in. x_out, out and add must not
+ * alias each other or the residual rows. Workspace as moe_layer_v1. */
+int moe_norm_layer_v1(const uint16_t* res_in, const uint16_t* add, const uint16_t* norm_w,
+                      float eps, uint16_t* res_out, uint16_t* x_out, int32_t T,
+                      const uint16_t* router_w, const float* logit_bias, int32_t top_k,
+                      const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                      const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                      uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
+                      void* stream);
+
 /* moe_layer_v1 without a workspace argument and without any allocation: the workspace is a
  * file-scope device array of moe_layer_noalloc_max_bytes_v1() bytes (64 MiB) per GPU, held until
  * the process ends. No counterpart in the reference: for callers that cannot call hipMalloc

@@ -42,6 +42,7 @@ EXPORTED = (
     "moe_rmsnorm_v1",
     "moe_layer_workspace_bytes_v1",
     "moe_layer_v1",
+    "moe_norm_layer_v1",
     "moe_fused_experts_v1",
     "moe_layer_noalloc_max_bytes_v1",
     "moe_layer_noalloc_v1",
@@ -137,6 +138,10 @@ _SIGS = {
     "moe_layer_v1": (
         [_P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P, _P, c_int64, _P, _P, _P,
          _I, _P],
+        c_int32),
+    "moe_norm_layer_v1": (
+        [_P, _P, _P, c_float, _P, _P, _I, _P, _P, _I, POINTER(ExpertSet), POINTER(ExpertSet), _P,
+         _P, c_int64, _P, _P, _P, _I, _P],
         c_int32),
     "moe_layer_noalloc_max_bytes_v1": ([], c_int64),
     "moe_layer_noalloc_v1": (

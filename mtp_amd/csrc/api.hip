@@ -435,7 +435,7 @@ int moe_rmsnorm_v1(uint16_t* res, const uint16_t* add, int32_t T, int32_t hidden
   if (T == 0) return MOE_OK;
   if (!res || !weight || !out) return fail(MOE_ERR_NULL, "rmsnorm: NULL pointer");
   if (out == res) return fail(MOE_ERR_SHAPE, "rmsnorm: out must not alias res");
-  MOE_CHECK_HIP(launch_rmsnorm(res, add, T, hidden, weight, eps, out, (hipStream_t)stream),
+  MOE_CHECK_HIP(launch_rmsnorm(res, add, T, hidden, weight, eps, res, out, (hipStream_t)stream),
                 "rmsnorm");
   return MOE_OK;
 }
@@ -448,15 +448,30 @@ int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_
   return (int64_t)layout(T, top_k, experts, has_shared ? 1 : 0, path).total;
 }
 
-int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const float* logit_bias,
-                 int32_t top_k, const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
-                 const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
-                 uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
-                 void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The decoder step's residual add + RMSNorm in front of a layer call (moe_norm_layer_v1).
+struct PreNorm {
+  const uint16_t* res_in;
+  const uint16_t* add;
+  const uint16_t* weight;
+  float eps;
+  uint16_t* res_out;
+  uint16_t* x_out;  // the layer's input
+};
+
+int layer_impl(const uint16_t* x, int32_t T, const uint16_t* router_w, const float* logit_bias,
+               int32_t top_k, const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+               const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+               uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
+               void* stream, const PreNorm* pn) {
   int rc = check_experts(experts, shared);
   if (rc) return rc;
   if (T < 0) return fail(MOE_ERR_SHAPE, "layer: T=%d", T);
   if (T == 0) return MOE_OK;
+  if (pn) x = pn->x_out;
   if (!x || !router_w || !out || !workspace) return fail(MOE_ERR_NULL, "layer: NULL pointer");
   if (shared && !shared_gate_w) return fail(MOE_ERR_NULL, "layer: shared expert needs shared_gate_w");
   const int E = experts->num_experts;
@@ -473,6 +488,12 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   float* logits = at<float>(workspace, L.logits);
   int32_t* ids = at<int32_t>(workspace, L.ids);
   float* w = at<float>(workspace, L.w);
+  // decode batches: the router normalises its own tokens; otherwise the norm runs first
+  const bool norm_in_router = pn && path == MOE_PATH_DECODE &&
+                              router_norm_fits(T, experts->hidden, pn->res_in, pn->res_out);
+  if (pn && !norm_in_router)
+    MOE_CHECK_HIP(launch_rmsnorm(pn->res_in, pn->add, T, experts->hidden, pn->weight, pn->eps,
+                                 pn->res_out, pn->x_out, s), "rmsnorm");
   if (path == MOE_PATH_PREFILL && router_prefill_fits(T, experts->hidden, E, top_k)) {
     // approximate MFMA logits, certified top-k with canonical logits for the selection
     MOE_CHECK_HIP(launch_router_prefill(x, T, experts->hidden, router_w, E,
@@ -483,9 +504,16 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
     if (rc) return rc;
     return copy_routing(ids, w, T, top_k, topk_ids_out, topk_weights_out, s);
   }
-  MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E,
-                                     shared ? shared_gate_w : nullptr, logit_bias, logits, s),
-                "router logits");
+  if (norm_in_router)
+    MOE_CHECK_HIP(launch_router_logits_norm(pn->res_in, pn->add, pn->weight, pn->eps, pn->res_out,
+                                            pn->x_out, T, experts->hidden, router_w, E,
+                                            shared ? shared_gate_w : nullptr, logit_bias, logits,
+                                            s),
+                  "rmsnorm + router logits");
+  else
+    MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E,
+                                       shared ? shared_gate_w : nullptr, logit_bias, logits, s),
+                  "router logits");
   // decode-size batches: with one or two tokens the MFMA decode kernels compute the top-k
   // themselves (slot grid; every W1 workgroup repeats it, which costs more than the launch it
   // saves beyond two tokens); up to 8 tokens top-k and align come from one block (no align
@@ -509,6 +537,44 @@ int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const f
   rc = run_experts(x, T, top_k, experts, shared, L, workspace, out, path, routing, s);
   if (rc) return rc;
   return copy_routing(ids, w, T, top_k, topk_ids_out, topk_weights_out, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_layer_v1(const uint16_t* x, int32_t T, const uint16_t* router_w, const float* logit_bias,
+                 int32_t top_k, const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                 const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                 uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
+                 void* stream) {
+  return layer_impl(x, T, router_w, logit_bias, top_k, experts, shared, shared_gate_w, workspace,
+                    workspace_bytes, out, topk_ids_out, topk_weights_out, path, stream, nullptr);
+}
+
+int moe_norm_layer_v1(const uint16_t* res_in, const uint16_t* add, const uint16_t* norm_w,
+                      float eps, uint16_t* res_out, uint16_t* x_out, int32_t T,
+                      const uint16_t* router_w, const float* logit_bias, int32_t top_k,
+                      const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                      const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
+                      uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
+                      void* stream) {
+  if (T < 0) return fail(MOE_ERR_SHAPE, "norm layer: T=%d", T);
+  if (T == 0) return MOE_OK;
+  if (!res_in || !norm_w || !res_out || !x_out) return fail(MOE_ERR_NULL, "norm layer: NULL pointer");
+  if (!experts) return fail(MOE_ERR_NULL, "experts is NULL");
+  const int H = experts->hidden;
+  if (H <= 0 || H % 8 != 0 || H > 8192)
+    return fail(MOE_ERR_SHAPE, "norm layer: hidden=%d (hidden %% 8 == 0, <= 8192)", H);
+  if (!(eps >= 0.0f)) return fail(MOE_ERR_SHAPE, "norm layer: eps must be >= 0");
+  if (x_out == res_in || x_out == res_out || (add && (x_out == add || res_out == add)))
+    return fail(MOE_ERR_SHAPE, "norm layer: x_out and add must not alias the residual rows");
+  if (out == x_out || out == res_in || out == res_out)
+    return fail(MOE_ERR_SHAPE, "norm layer: out must not alias x_out or the residual rows");
+  const PreNorm pn{res_in, add, norm_w, eps, res_out, x_out};
+  return layer_impl(nullptr, T, router_w, logit_bias, top_k, experts, shared, shared_gate_w,
+                    workspace, workspace_bytes, out, topk_ids_out, topk_weights_out, path, stream,
+                    &pn);
 }
 
 int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,

@@ -140,9 +140,20 @@ hipError_t launch_predictor(const uint16_t* h, int T, int H, int L, const uint16
                             const uint16_t* w2, int E, int top_k, float* z1, uint16_t* a,
                             float* z2, int32_t* ids, float* scores, hipStream_t stream);
 
-// Residual add (add nullable) and (1 + w) RMSNorm per token row, hidden % 8 == 0, <= 8192.
-hipError_t launch_rmsnorm(uint16_t* res, const uint16_t* add, int T, int H, const uint16_t* w,
-                          float eps, uint16_t* out, hipStream_t stream);
+// Residual add (add nullable) and (1 + w) RMSNorm per token row, hidden % 8 == 0, <= 8192:
+// res_out = res_in + add, out = norm(res_out); res_out may be res_in.
+hipError_t launch_rmsnorm(const uint16_t* res_in, const uint16_t* add, int T, int H,
+                          const uint16_t* w, float eps, uint16_t* res_out, uint16_t* out,
+                          hipStream_t stream);
+// Decode router with the residual add + RMSNorm of its tokens folded in (router.hip): writes
+// res_out, x_out (the launch_rmsnorm bits) and the logits (the launch_router_logits bits of
+// x_out). T <= 64, H <= 2048, res_out != res_in.
+bool router_norm_fits(int T, int H, const void* res_in, const void* res_out);
+hipError_t launch_router_logits_norm(const uint16_t* res_in, const uint16_t* add,
+                                     const uint16_t* norm_w, float eps, uint16_t* res_out,
+                                     uint16_t* x_out, int T, int H, const uint16_t* W, int E,
+                                     const uint16_t* shared_w, const float* bias, float* logits,
+                                     hipStream_t stream);
 
 // Block sizes (slots per block) of the two paths.
 constexpr int kDecodeBlockM = 16;

@@ -13,6 +13,7 @@
 //    the ids stay in LDS between the two steps, so no cross-block visibility is needed and the
 //    align launch disappears.
 #include "launch.h"
+#include "norm_row.h"
 #include "routing.h"
 
 namespace {
@@ -30,6 +31,67 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const int e0 = (wave % tiles_e) * TE;
   if (t0 >= T) return;
   logits_tile<TT, TE>(x, T, H, W, E, shared_w, bias, logits, t0, e0, lane);
+}
+
+// Router of a decoder step with the step's residual add + RMSNorm folded in: workgroup = one
+// tile of TT tokens x (4 waves x TE) router rows. The waves first issue the loads of their
+// router rows, then the workgroup normalises its TT tokens into LDS (norm_row, the bits of the
+// norm kernel); the first workgroup of each token tile also writes the updated residual and the
+// normalised rows (the layer's input for W1). res_out must not be res_in: the other workgroups
+// of the tile still read res_in. H <= 2048.
+template <int TT, int TE>
+__global__ __launch_bounds__(kNormThreads) void router_logits_norm_kernel(
+    const uint16_t* __restrict__ res_in, const uint16_t* __restrict__ add,
+    const uint16_t* __restrict__ norm_w, float eps, uint16_t* __restrict__ res_out,
+    uint16_t* __restrict__ x_out, int T, int H, const uint16_t* __restrict__ W, int E,
+    const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
+    float* __restrict__ logits) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[TT * kNormChunk];
+  __shared__ float s_part[TT * (kNormThreads / 64)];
+  const int rows = E + (shared_w ? 1 : 0);
+  const int tiles_e = (rows + TE - 1) / TE;
+  const int groups = (tiles_e + 3) / 4;  // workgroups per token tile
+  const int tt = (int)blockIdx.x / groups, eg = (int)blockIdx.x % groups;
+  const int t0 = tt * TT;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int e_tile = eg * 4 + wave;
+  LdsLogitsTile<TT, TE> tile;
+  if (e_tile < tiles_e) tile.load(H, W, E, shared_w, e_tile * TE, lane);
+  const bool writer = eg == 0;
+  const uint16_t* rin[TT];
+  const uint16_t* ad[TT];
+  bool valid[TT];
+  uint16_t* rout[TT];
+  uint16_t* xo[TT];
+#pragma unroll
+  for (int i = 0; i < TT; ++i) {
+    const int t = t0 + i;
+    valid[i] = t < T;
+    const int64_t o = (int64_t)(valid[i] ? t : 0) * H;
+    rin[i] = res_in + o;
+    ad[i] = add ? add + o : nullptr;
+    rout[i] = writer && valid[i] ? res_out + o : nullptr;
+    xo[i] = writer && valid[i] ? x_out + o : nullptr;
+  }
+  norm_rows<TT, 1>(rin, ad, valid, H, norm_w, eps, s_part, s_x, rout, xo);
+  __syncthreads();  // the s_x rows are complete
+  if (e_tile < tiles_e)
+    tile.compute_store(s_x, T, H, E, shared_w != nullptr, bias, logits, t0, e_tile * TE, lane);
+}
+
+template <int TT, int TE>
+hipError_t launch_logits_norm(const uint16_t* res_in, const uint16_t* add, const uint16_t* norm_w,
+                              float eps, uint16_t* res_out, uint16_t* x_out, int T, int H,
+                              const uint16_t* W, int E, const uint16_t* shared_w,
+                              const float* bias, float* logits, hipStream_t stream) {
+  const int rows = E + (shared_w ? 1 : 0);
+  const int groups = ((rows + TE - 1) / TE + 3) / 4;
+  const int blocks = (T + TT - 1) / TT * groups;
+  hipLaunchKernelGGL((router_logits_norm_kernel<TT, TE>), dim3(blocks), dim3(kNormThreads), 0,
+                     stream, res_in, add, norm_w, eps, res_out, x_out, T, H, W, E, shared_w, bias,
+                     logits);
+  return hipGetLastError();
 }
 
 // Prefill-size logits: one wave per 8 x 8 (token x router-row) tile, H a multiple of 512 (one
@@ -235,6 +297,23 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
     return hipGetLastError();
   }
   return launch_logits_tiled<8, 8>(x, T, H, W, E, shared_w, bias, logits, stream);
+}
+
+bool router_norm_fits(int T, int H, const void* res_in, const void* res_out) {
+  return T >= 1 && T <= 64 && H >= 8 && H <= kNormChunk && H % 8 == 0 && res_in != res_out;
+}
+
+hipError_t launch_router_logits_norm(const uint16_t* res_in, const uint16_t* add,
+                                     const uint16_t* norm_w, float eps, uint16_t* res_out,
+                                     uint16_t* x_out, int T, int H, const uint16_t* W, int E,
+                                     const uint16_t* shared_w, const float* bias, float* logits,
+                                     hipStream_t stream) {
+  if (!router_norm_fits(T, H, res_in, res_out)) return hipErrorInvalidValue;
+  if (T <= 4)  // the tiles of launch_router_logits
+    return launch_logits_norm<1, 2>(res_in, add, norm_w, eps, res_out, x_out, T, H, W, E,
+                                    shared_w, bias, logits, stream);
+  return launch_logits_norm<2, 4>(res_in, add, norm_w, eps, res_out, x_out, T, H, W, E, shared_w,
+                                  bias, logits, stream);
 }
 
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,

@@ -105,6 +105,94 @@ MOE_DEV void logits_tile(const uint16_t* __restrict__ x, int T, int H, const uin
   }
 }
 
+// logits_tile for H <= 2048 with the TT token rows in LDS (x_lds [TT][H] bf16, rows t0 ..
+// t0 + TT - 1 of the batch), in two phases: load() issues every chunk of the wave's TE router
+// rows (no dependence on x), compute_store() runs the same chunks per lane, fma order and
+// butterfly as logits_tile, so the logits are bit-identical to logits_tile on the same rows.
+template <int TT, int TE>
+struct LdsLogitsTile {
+  static constexpr int NI = 4;  // 64 * NI chunks of 8 = 2048 columns
+  u32x4 wv[NI][TE];
+
+  MOE_DEV void load(int H, const uint16_t* __restrict__ W, int E,
+                    const uint16_t* __restrict__ shared_w, int e0, int lane) {
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W, (uint32_t)E * (uint32_t)H * 2u);
+    const __amdgpu_buffer_rsrc_t sr = buf_rsrc(shared_w, shared_w ? (uint32_t)H * 2u : 0u);
+    const int nq = H / 8;
+#pragma unroll
+    for (int j = 0; j < TE; ++j) {
+      const int e = e0 + j;
+      const uint32_t wo =
+          e < E ? (uint32_t)e * (uint32_t)H * 2u : (e == E && shared_w ? 0u : kOutOfRange);
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const int q = 64 * it + lane;
+        const uint32_t qo = q < nq ? (uint32_t)q * 16u : kOutOfRange;
+        wv[it][j] = buf_ld128(e == E ? sr : wr, (wo + qo) | (qo & kOutOfRange));
+      }
+    }
+  }
+
+  MOE_DEV void compute_store(const uint16_t* x_lds, int T, int H, int E, bool has_shared,
+                             const float* __restrict__ bias, float* __restrict__ logits, int t0,
+                             int e0, int lane) const {
+    const int rows = E + (has_shared ? 1 : 0), nq = H / 8;
+    float acc[TT][TE];
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+      for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int q = 64 * it + lane;
+      if (q >= nq) continue;
+      u32x4 xv[TT];
+#pragma unroll
+      for (int i = 0; i < TT; ++i) xv[i] = ld128(x_lds + i * H + 8 * q);
+#pragma unroll
+      for (int el = 0; el < 8; ++el) {
+        float wf[TE];
+#pragma unroll
+        for (int j = 0; j < TE; ++j)
+          wf[j] = (el & 1) ? bf16hi_to_f32(wv[it][j][el >> 1]) : bf16lo_to_f32(wv[it][j][el >> 1]);
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+          const uint32_t xd = xv[i][el >> 1];
+          const float xf = (el & 1) ? bf16hi_to_f32(xd) : bf16lo_to_f32(xd);
+#pragma unroll
+          for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xf, wf[j], acc[i][j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+      for (int j = 0; j < TE; ++j) {
+        float v = acc[i][j];
+        v = wave_xor_sum(v, 32);
+        v = wave_xor_sum(v, 16);
+        v = wave_xor_sum(v, 8);
+        v = wave_xor_sum(v, 4);
+        v = wave_xor_sum(v, 2);
+        v = wave_xor_sum(v, 1);
+        acc[i][j] = v;
+      }
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) {
+          const int t = t0 + i, e = e0 + j;
+          if (t < T && e < rows) {
+            float v = acc[i][j];
+            if (bias && e < E) v = v + bias[e];
+            logits[(int64_t)t * (E + 1) + e] = v;
+          }
+        }
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------- top-k
 // 32-bit order key of a logit: unsigned order = logit order, with -0 equal to +0 and NaN (key 1)
 // below every number; key 0 marks "not a candidate" (already selected, or past E).

@@ -296,6 +296,53 @@ def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, t
     return out
 
 
+def norm_layer(res: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts,
+               norm_w: torch.Tensor, *, add: torch.Tensor | None = None, eps: float = 1e-6,
+               res_out: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+               top_k: int = 8, logit_bias: torch.Tensor | None = None,
+               shared: MoeExperts | None = None, shared_gate_w: torch.Tensor | None = None,
+               path: str | int = "auto", workspace: torch.Tensor | None = None,
+               out: torch.Tensor | None = None):
+    """A decoder step: res_out = res + add, x = rmsnorm(res_out) * (1 + norm_w), then the routed
+    layer on x (moe_norm_layer_v1; the bits of ``rmsnorm`` followed by ``moe_layer``). Returns
+    (out, res_out, x). res_out defaults to a new tensor (a distinct buffer lets decode batches
+    normalise inside the router); pass ``res`` itself to update it in place."""
+    lib = _lib.load()
+    _bf16_matrix(res, "res", experts.hidden_size)
+    _bf16_matrix(router_w, "router_w", experts.hidden_size)
+    T, H = res.shape
+    if add is not None:
+        _bf16_matrix(add, "add", H)
+        if add.shape[0] != T:
+            raise ValueError(f"add has {add.shape[0]} rows for {T}")
+    if norm_w.dtype != torch.bfloat16 or norm_w.numel() != H or not norm_w.is_contiguous():
+        raise ValueError("norm_w must be a contiguous bfloat16 tensor of hidden elements")
+    if (shared is None) != (shared_gate_w is None):
+        raise ValueError("shared and shared_gate_w must be given together")
+    _require_gpu(res, add, norm_w, router_w)
+    if res_out is None:
+        res_out = torch.empty_like(res)
+    if x_out is None:
+        x_out = torch.empty_like(res)
+    if out is None:
+        out = torch.empty_like(res)
+    for t, name in ((res_out, "res_out"), (x_out, "x_out"), (out, "out")):
+        if t.shape != res.shape or t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 tensor shaped like res")
+    p = _path(path)
+    need = workspace_bytes(T, top_k, experts, shared is not None, p)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=res.device)
+    ex = experts.struct()
+    sh = shared.struct() if shared is not None else None
+    _lib.check(lib.moe_norm_layer_v1(
+        res.data_ptr(), _ptr(add), norm_w.data_ptr(), float(eps), res_out.data_ptr(),
+        x_out.data_ptr(), T, router_w.data_ptr(), _ptr(logit_bias), top_k, ctypes.byref(ex),
+        ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
+        workspace.numel(), out.data_ptr(), None, None, p, _stream()))
+    return out, res_out, x_out
+
+
 def fused_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                   experts: MoeExperts, *, shared: MoeExperts | None = None,
                   shared_gate_w: torch.Tensor | None = None, path: str | int = "auto",

@@ -85,3 +85,58 @@ def test_decode_chain_through_norm():
         want_res, want_h = moe_ref.rmsnorm_ref(res_bits, _bits(norm_w[l + 1]), add_bits=_bits(y))
         assert np.array_equal(_bits(res), want_res)
         _within_one_ulp(_bits(h), want_h)
+
+
+@pytest.mark.parametrize("T,shared,with_add,in_place,path", [
+    (1, False, True, False, "decode"), (2, True, True, False, "decode"),
+    (5, False, False, False, "decode"), (16, False, True, False, "decode"),
+    (64, True, True, False, "decode"), (7, False, True, True, "decode"),
+    (300, False, True, False, "auto")])
+def test_norm_layer_equals_norm_then_layer(T, shared, with_add, in_place, path):
+    """moe_norm_layer_v1 gives the bits of moe_rmsnorm_v1 followed by moe_layer_v1: on decode
+    batches the router normalises its own tokens (same arithmetic as the norm kernel); in place
+    (res_out == res_in) and on the prefill path the norm kernel runs first."""
+    _say(f"norm layer T={T} shared={shared} add={with_add} in_place={in_place} path={path}")
+    layer = to_gpu(synth.make_layer(8, zipf=True, shared=shared))
+    g = torch.Generator().manual_seed(T + 101)
+    res = torch.randn(T, 2048, generator=g).to(torch.bfloat16).cuda()
+    add = (0.5 * torch.randn(T, 2048, generator=g)).to(torch.bfloat16).cuda() if with_add else None
+    nw = (0.05 * torch.randn(2048, generator=g)).to(torch.bfloat16).cuda()
+    kw = dict(logit_bias=layer.logit_bias, path=path)
+    if shared:
+        kw.update(shared=layer.shared, shared_gate_w=layer.shared_gate_w)
+    # reference: the norm kernel, then the layer
+    res_ref = res.clone()
+    x_ref = ops.rmsnorm(res_ref, nw, add=add, eps=1e-6)
+    y_ref = ops.moe_layer(x_ref, layer.router_w, layer.experts, **kw)
+    res_in = res.clone()
+    y, res_out, x = ops.norm_layer(res_in, layer.router_w, layer.experts, nw, add=add, eps=1e-6,
+                                   res_out=res_in if in_place else None, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(x, x_ref)
+    assert torch.equal(res_out, res_ref)
+    assert torch.equal(y, y_ref)
+    if not in_place:
+        assert torch.equal(res_in, res)  # the input residual is left as it was
+
+
+def test_norm_layer_chain_equals_unfused_chain():
+    """Three chained decode steps (batch 4) through moe_norm_layer_v1 with two alternating
+    residual buffers give the bits of the rmsnorm + moe_layer chain."""
+    _say("norm layer chain")
+    layers = [to_gpu(synth.make_layer(20 + l, zipf=True)) for l in range(3)]
+    g = torch.Generator().manual_seed(5)
+    res0 = torch.randn(4, 2048, generator=g).to(torch.bfloat16).cuda()
+    nws = [(0.05 * torch.randn(2048, generator=g)).to(torch.bfloat16).cuda() for _ in range(3)]
+    res_a, y_a = res0.clone(), None
+    for ly, nw in zip(layers, nws):
+        x = ops.rmsnorm(res_a, nw, add=y_a)
+        y_a = ops.moe_layer(x, ly.router_w, ly.experts, logit_bias=ly.logit_bias, path="decode")
+    bufs, y_b, cur = [res0.clone(), torch.empty_like(res0)], None, 0
+    for ly, nw in zip(layers, nws):
+        y_b, _, _ = ops.norm_layer(bufs[cur], ly.router_w, ly.experts, nw, add=y_b,
+                                   res_out=bufs[1 - cur], logit_bias=ly.logit_bias, path="decode")
+        cur = 1 - cur
+    torch.cuda.synchronize()
+    assert torch.equal(y_b, y_a)
+    assert torch.equal(bufs[cur], res_a)
