@@ -508,6 +508,7 @@ def offload_bench(layers, args, dev) -> dict:
     torch.cuda.synchronize()
     log(f"[bench] offload: host pool {pool.host.nbytes / 1e9:.2f} GB pinned, HBM pool "
         f"{pool.device_pool.numel() / 1e9:.2f} GB, filled in {time.time() - t0:.1f}s")
+    calib = h2d_calibration(pool)
     gen = torch.Generator(device=dev)
     gen.manual_seed(5000)
     w1 = (torch.randn(L, D, H, generator=gen, device=dev) / H ** 0.5).to(torch.bfloat16)
@@ -585,7 +586,68 @@ def offload_bench(layers, args, dev) -> dict:
                     "(width 256, 4 future deltas; delta 0 used); ready-late = first demand of a "
                     "prefetched expert whose copy completed after the demand (HIP event times)",
         "runs": runs,
+        "h2d_calibration": calib,
     }
+
+
+def h2d_calibration(pool, reps: int = 200) -> dict:
+    """Pinned host -> HBM copy of expert blobs with hipMemcpyAsync (the slot cache's copy), timed
+    with HIP events on one stream: single blobs and batches of 8, p50 / p95, beside the reference's
+    measured copy (W7900, PCIe 4.0 x16)."""
+    import ctypes
+
+    import torch
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                   ctypes.c_void_p]
+    hip.hipMemcpyAsync.restype = ctypes.c_int
+    blob, n_blobs = pool.blob, pool.num_layers * pool.num_experts
+    dst = pool.device_pool.view(-1)
+    n_dst = dst.numel() // blob
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    def copy(i: int) -> None:
+        src = pool.host.ptr + (i * 7919 % n_blobs) * blob  # blobs spread over the pool
+        err = hip.hipMemcpyAsync(ctypes.c_void_p(dst.data_ptr() + (i % n_dst) * blob),
+                                 ctypes.c_void_p(src), blob, 1, sh)  # 1 = host to device
+        if err != 0:
+            raise RuntimeError(f"hipMemcpyAsync failed with HIP error {err}")
+
+    def timed(n: int, rep: int) -> float:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for j in range(n):
+            copy(rep * n + j)
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) * 1e3  # us
+
+    for r in range(10):
+        timed(8, r)
+    one = [timed(1, r) for r in range(reps)]
+    eight = [timed(8, r) for r in range(reps // 2)]
+    out = {
+        "expert_bytes": blob,
+        "one_expert_us": {"p50": statistics.median(one), "p95": pct(one, 0.95)},
+        "one_expert_GBps_p95": blob / pct(one, 0.95) / 1e3,
+        "one_expert_GBps_p50": blob / statistics.median(one) / 1e3,
+        "eight_experts_us_per_expert": {"p50": statistics.median(eight) / 8,
+                                        "p95": pct(eight, 0.95) / 8},
+        "eight_experts_GBps_p50": 8 * blob / statistics.median(eight) / 1e3,
+        "samples": {"one": len(one), "eight": len(eight)},
+        "reference_w7900_pcie4": {"one_expert_GBps_p95": 20.43, "eight_experts_GBps_p50": 28.23,
+                                  "eight_experts_us_per_expert_p95": 62.09,
+                                  "expert_bytes": 1.65e6,
+                                  "source": "PROGRESS.md:48610-48612"},
+    }
+    log(f"[bench] H2D calibration: 1 expert ({blob / 1e6:.2f} MB) p50 {out['one_expert_us']['p50']:.1f} us "
+        f"p95 {out['one_expert_us']['p95']:.1f} us ({out['one_expert_GBps_p95']:.1f} GB/s at p95); "
+        f"8 experts {out['eight_experts_GBps_p50']:.1f} GB/s at p50, "
+        f"{out['eight_experts_us_per_expert']['p95']:.1f} us per expert at p95")
+    return out
 
 
 CPU_REPS = 5
