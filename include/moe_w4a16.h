@@ -372,6 +372,22 @@ int moe_slot_cache_stats_v1(uint64_t handle, moe_slot_cache_counters_v1* out);
 /* Slot of (layer, expert), -1 if absent, -2 for a bad handle or index. */
 int moe_slot_cache_slot_of_v1(uint64_t handle, int32_t layer, int32_t expert);
 
+/* One offloaded MoE layer of a decode step in one call: router logits and top-k into the
+ * workspace, the routed ids to ids_host (pinned host, T * top_k; the call waits for them on
+ * stream), moe_slot_cache_demand_v1, the routed experts from the layer's slots (experts = the
+ * layer's slot view, as for moe_fused_experts_v1), moe_slot_cache_layer_done_v1 and, when
+ * n_prefetch > 0, moe_slot_cache_prefetch_v1 of the host list prefetch. Replaces the per-layer
+ * sequence of the reference's offloaded decode (router top-k, then
+ * ControlledExpertCacheManager.demand, cache_manager.py:233-247, then the expert MLPs, then
+ * issue_prefetch, :222-231) with one host call. Workspace as moe_layer_v1 (no shared expert).
+ * hits: NULL or the demand's hits. */
+int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32_t T,
+                         const uint16_t* router_w, const float* logit_bias, int32_t top_k,
+                         const moe_expert_set_v1* experts, void* workspace,
+                         int64_t workspace_bytes, uint16_t* out, int32_t* ids_host,
+                         const int32_t* prefetch, int32_t n_prefetch, int32_t path, void* stream,
+                         int32_t* hits);
+
 #ifdef __cplusplus
 }
 #endif

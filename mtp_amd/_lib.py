@@ -58,6 +58,7 @@ EXPORTED = (
     "moe_slot_cache_layer_done_v1",
     "moe_slot_cache_stats_v1",
     "moe_slot_cache_slot_of_v1",
+    "moe_offload_layer_v1",
 )
 
 
@@ -163,6 +164,10 @@ _SIGS = {
     "moe_slot_cache_layer_done_v1": ([ctypes.c_uint64, _I], c_int32),
     "moe_slot_cache_stats_v1": ([ctypes.c_uint64, POINTER(SlotCacheCounters)], c_int32),
     "moe_slot_cache_slot_of_v1": ([ctypes.c_uint64, _I, _I], c_int32),
+    "moe_offload_layer_v1": (
+        [ctypes.c_uint64, _I, _P, _I, _P, _P, _I, POINTER(ExpertSet), _P, c_int64, _P, _P, _P, _I,
+         _I, _P, POINTER(c_int32)],
+        c_int32),
 }
 
 

@@ -612,4 +612,52 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
   return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, routing, s);
 }
 
+int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32_t T,
+                         const uint16_t* router_w, const float* logit_bias, int32_t top_k,
+                         const moe_expert_set_v1* experts, void* workspace,
+                         int64_t workspace_bytes, uint16_t* out, int32_t* ids_host,
+                         const int32_t* prefetch, int32_t n_prefetch, int32_t path, void* stream,
+                         int32_t* hits) {
+  int rc = check_experts(experts, nullptr);
+  if (rc) return rc;
+  if (T < 1) return fail(MOE_ERR_SHAPE, "offload layer: T=%d", T);
+  if (!x || !router_w || !out || !workspace || !ids_host || (n_prefetch > 0 && !prefetch))
+    return fail(MOE_ERR_NULL, "offload layer: NULL pointer");
+  const int E = experts->num_experts;
+  if (top_k < 1 || top_k > E || top_k > 64)
+    return fail(MOE_ERR_SHAPE, "offload layer: top_k=%d outside [1, min(num_experts, 64)]", top_k);
+  if (n_prefetch < 0) return fail(MOE_ERR_SHAPE, "offload layer: n_prefetch=%d", n_prefetch);
+  const int path_in = path;
+  path = resolve_path(path, T, top_k);
+  if (path < 0) return fail(MOE_ERR_UNSUPPORTED, "offload layer: unknown path %d", path_in);
+  const Workspace L = layout(T, top_k, experts, 0, path);
+  if (workspace_bytes < (int64_t)L.total)
+    return fail(MOE_ERR_WORKSPACE, "offload layer: workspace %lld < required %lld",
+                (long long)workspace_bytes, (long long)L.total);
+  hipStream_t s = (hipStream_t)stream;
+  float* logits = at<float>(workspace, L.logits);
+  int32_t* ids = at<int32_t>(workspace, L.ids);
+  float* w = at<float>(workspace, L.w);
+  const int n = T * top_k;
+  MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E, nullptr, logit_bias,
+                                     logits, s), "offload layer: router logits");
+  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, 0, ids, w, s),
+                "offload layer: router topk");
+  // the host-managed cache needs the routed ids: the one wait of the layer
+  MOE_CHECK_HIP(hipMemcpyAsync(ids_host, ids, (size_t)n * 4, hipMemcpyDeviceToHost, s),
+                "offload layer: ids to the host");
+  MOE_CHECK_HIP(hipStreamSynchronize(s), "offload layer: wait for the ids");
+  rc = moe_slot_cache_demand_v1(cache, layer, ids_host, n, stream, hits);
+  if (rc) return rc;
+  const Routing routing =
+      (path == MOE_PATH_DECODE && slot_grid_fits(T, top_k, 0)) ? ROUTE_GRID_IDS : ROUTE_ALIGN;
+  rc = run_experts(x, T, top_k, experts, nullptr, L, workspace, out, path, routing, s);
+  if (rc) return rc;
+  rc = moe_slot_cache_layer_done_v1(cache, layer);
+  if (rc) return rc;
+  if (n_prefetch > 0)
+    return moe_slot_cache_prefetch_v1(cache, layer, prefetch, n_prefetch, stream, nullptr);
+  return MOE_OK;
+}
+
 }  // extern "C"

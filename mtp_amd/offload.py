@@ -318,21 +318,36 @@ class OffloadedExperts:
 def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts, layer: int, *,
                  top_k: int = 8, logit_bias: torch.Tensor | None = None,
                  ids_host: torch.Tensor | None = None, path: str = "auto",
-                 workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """One offloaded MoE layer: router -> ids to the host -> demand -> experts from the slots.
+                 workspace: torch.Tensor | None = None,
+                 prefetch: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One offloaded MoE layer in one native call (moe_offload_layer_v1): router -> ids to the
+    host -> demand -> experts from the slots -> layer_done [-> prefetch of `prefetch`].
 
     The host wait for the routed ids is the one synchronisation per layer that a host-managed
     cache needs (the reference's demand() is a host call on the routed ids too,
     cache_manager.py:233-247). Returns (out bf16 [T, H], routed ids on the host int32 [T, k]).
     """
-    ids, w, _, _ = ops.router_topk(x, router_w, top_k, logit_bias=logit_bias)
-    if ids_host is None or ids_host.shape != ids.shape:
-        ids_host = torch.empty(ids.shape, dtype=torch.int32, pin_memory=True)
-    ids_host.copy_(ids, non_blocking=True)
-    torch.cuda.current_stream().synchronize()
-    pool.demand(layer, ids_host.reshape(-1).tolist())
-    out = ops.fused_experts(x, ids, w, pool.layer_experts(layer), path=path, workspace=workspace)
-    pool.layer_done(layer)
+    lib = _lib.load()
+    ex = pool.layer_experts(layer)
+    ops._bf16_matrix(x, "input", ex.hidden_size)
+    ops._bf16_matrix(router_w, "router_w", ex.hidden_size)
+    if router_w.shape[0] != ex.num_experts:
+        raise ValueError(f"router_w has {router_w.shape[0]} rows for {ex.num_experts} experts")
+    ops._require_gpu(x, router_w, logit_bias)
+    T = x.shape[0]
+    p = ops._path(path)
+    need = ops.workspace_bytes(T, top_k, ex, False, p)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    if ids_host is None or tuple(ids_host.shape) != (T, top_k):
+        ids_host = torch.empty((T, top_k), dtype=torch.int32, pin_memory=True)
+    out = torch.empty_like(x)
+    arr, n = SlotCache._ids(prefetch or [])
+    st = ex.struct()
+    _lib.check(lib.moe_offload_layer_v1(
+        pool.cache.handle, layer, x.data_ptr(), T, router_w.data_ptr(), ops._ptr(logit_bias),
+        top_k, ctypes.byref(st), workspace.data_ptr(), workspace.numel(), out.data_ptr(),
+        ids_host.data_ptr(), arr, n, p, ops._stream(), None))
     return out, ids_host
 
 
@@ -405,8 +420,7 @@ class OffloadDecoder:
         for l in range(self.pool.num_layers):
             out, self._ids_host = routed_layer(x, self.routers[l], self.pool, l, top_k=self.top_k,
                                                logit_bias=self.biases[l], ids_host=self._ids_host,
-                                               path=self.path, workspace=self._ws)
-            if prefetch is not None and prefetch[l]:
-                self.pool.prefetch(l, prefetch[l])
+                                               path=self.path, workspace=self._ws,
+                                               prefetch=prefetch[l] if prefetch is not None else None)
             outs.append(out)
         return outs

@@ -92,6 +92,36 @@ def test_routed_layer_matches_oracle(pooled):
     assert moe_ref.rel_err(out.float().cpu().numpy(), ref) <= LAYER_RTOL
 
 
+@pytest.mark.parametrize("T,path", [(1, "decode"), (2, "decode"), (2, "prefill")])
+def test_offload_layer_call_matches_resident_layer(pooled, T, path):
+    """moe_offload_layer_v1 (router, ids to the host, demand, the experts from the slots,
+    layer_done and the prefetch list in one call) gives the resident layer's ids and output
+    bit for bit, counts the demand, and the prefetched experts that are resident afterwards
+    hold their host bytes."""
+    _say(f"offload layer call T={T} path={path}")
+    layers, pool = pooled
+    layer = 1
+    g = layers[layer]
+    x = synth.make_tokens(T, 512, seed=90 + T).cuda()
+    before = pool.stats()
+    out, ids_host = routed_layer(x, g.router_w, pool, layer, top_k=4, logit_bias=g.logit_bias,
+                                 prefetch=[7, 8, 9], path=path)
+    want, ids, _ = ops.moe_layer(x, g.router_w, g.experts, top_k=4, logit_bias=g.logit_bias,
+                                 path=path, return_routing=True)
+    torch.cuda.synchronize()
+    after = pool.stats()
+    assert np.array_equal(ids_host.numpy(), ids.cpu().numpy())
+    assert torch.equal(out, want)
+    assert after["demand_count"] - before["demand_count"] == T * 4
+    _slot_bytes_ok(pool, layer, ids_host.reshape(-1).tolist(), pack_blobs(g.experts))
+    issued = after["issued_fetch_count"] - before["issued_fetch_count"]
+    skipped = after["prefetch_skipped_pinned_count"] - before["prefetch_skipped_pinned_count"]
+    assert issued + skipped <= 3
+    assert after["prefetch_bytes"] - before["prefetch_bytes"] == issued * pool.blob
+    resident = [e for e in (7, 8, 9) if pool.cache.slot_of(layer, e) >= 0]
+    _slot_bytes_ok(pool, layer, resident, pack_blobs(g.experts))
+
+
 @pytest.mark.parametrize("T,L,H,D,E,k", [(1, 3, 512, 256, 64, 16), (4, 2, 2048, 1024, 256, 16),
                                           (3, 1, 256, 64, 40, 5)])
 def test_predictor_matches_oracle(T, L, H, D, E, k):
