@@ -80,6 +80,19 @@ def test_prefill_shapes_and_groups(E, H, I, G, T, shared):
     _check_layer(layer, T, 4, "prefill")
 
 
+@pytest.mark.parametrize("E,H,I,G,shared", [(32, 1024, 512, 128, False), (24, 1024, 256, 64, True),
+                                             (20, 1536, 1024, 256, False)])
+@pytest.mark.parametrize("T", [1, 2, 5, 40])
+def test_decode_shapes_and_groups(E, H, I, G, shared, T):
+    """Decode path over other hidden / intermediate / group sizes: hidden 1024 gives the fused
+    W1 + W2 slot grid four waves over K (hidden / 256); groups 64 and 256 and hidden 1536 take
+    the unfused slot grid; 5 and 40 tokens the blocked kernels and the token-sum W2."""
+    _say(f"decode shape E={E} H={H} I={I} G={G} shared={shared} T={T}")
+    layer = synth.make_layer(4, num_experts=E, hidden=H, intermediate=I, zipf=True, shared=shared,
+                             group=G)
+    _check_layer(layer, T, 4, "decode")
+
+
 @pytest.mark.parametrize("T", [1, 32])
 def test_config4_shared_expert(T):
     """Config 4: routed top-8 plus a sigmoid-gated int4 shared expert."""

@@ -120,6 +120,28 @@ def test_norm_layer_equals_norm_then_layer(T, shared, with_add, in_place, path):
         assert torch.equal(res_in, res)  # the input residual is left as it was
 
 
+@pytest.mark.parametrize("T,H", [(1, 1024), (6, 1024), (3, 512)])
+def test_norm_layer_narrow_hidden(T, H):
+    """The router's folded norm over rows shorter than its 2048-column tile (fewer chunks per
+    lane) still gives the bits of the norm kernel followed by the layer."""
+    _say(f"norm layer narrow hidden T={T} H={H}")
+    layer = to_gpu(synth.make_layer(9, num_experts=32, hidden=H, intermediate=512, zipf=True))
+    g = torch.Generator().manual_seed(T + 7 * H)
+    res = torch.randn(T, H, generator=g).to(torch.bfloat16).cuda()
+    add = (0.5 * torch.randn(T, H, generator=g)).to(torch.bfloat16).cuda()
+    nw = (0.05 * torch.randn(H, generator=g)).to(torch.bfloat16).cuda()
+    res_ref = res.clone()
+    x_ref = ops.rmsnorm(res_ref, nw, add=add, eps=1e-6)
+    y_ref = ops.moe_layer(x_ref, layer.router_w, layer.experts, top_k=4,
+                          logit_bias=layer.logit_bias, path="decode")
+    y, res_out, x = ops.norm_layer(res.clone(), layer.router_w, layer.experts, nw, add=add,
+                                   eps=1e-6, top_k=4, logit_bias=layer.logit_bias, path="decode")
+    torch.cuda.synchronize()
+    assert torch.equal(x, x_ref)
+    assert torch.equal(res_out, res_ref)
+    assert torch.equal(y, y_ref)
+
+
 def test_norm_layer_chain_equals_unfused_chain():
     """Three chained decode steps (batch 4) through moe_norm_layer_v1 with two alternating
     residual buffers give the bits of the rmsnorm + moe_layer chain."""
