@@ -176,3 +176,46 @@ def test_dequantize_host_tensors_on_the_gpu(store_dir):
     want = gptq_ref.dequant_f32(ex.gate.qweight[1].numpy(), ex.gate.qzeros[1].numpy(),
                                 f16_bits(ex.gate.scales[1]), linear_weight=False)
     assert np.array_equal(out.numpy(), want.astype(np.float16))
+
+
+@pytest.mark.parametrize("dtype_name,mode", [("bf16", "softmax"), ("fp16", "raw")])
+def test_trace_harness_call_sequence(store_dir, tmp_path, dtype_name, mode):
+    """The call sequence of the reference's trace smoke harness
+    (scripts/smoke_trace_topk_expert_mlp.py:60-137) on a synthetic trace sample: resolve the
+    sample through a manifest, load the payload, select one token's router top-k and weights,
+    load those experts, take the token's hidden state ([1, 1, H]) as input, and run the module
+    with long ids and weights in the harness dtype. The output is checked against the oracle."""
+    import json
+
+    from mtp_amd.repack import resolve_torch_dtype
+    from mtp_amd.tracing import (load_trace_payload, resolve_trace_sample, select_router_topk,
+                                 select_trace_hidden_token)
+    d, ex = store_dir
+    target = resolve_torch_dtype(dtype_name)
+    g = torch.Generator().manual_seed(33)
+    ids = torch.stack([torch.randperm(E, generator=g)[:4] for _ in range(3)]).view(1, 3, 4)
+    payload = {"router_topk": {"model.layers.0.mlp.gate": [ids]},
+               "router_scores": {"model.layers.0.mlp.gate": [torch.rand(1, 3, 4, generator=g)]},
+               "last_hidden_state": torch.randn(1, 3, H, generator=g)}
+    (tmp_path / "s").mkdir()
+    torch.save(payload, tmp_path / "s" / "sample.pt")
+    (tmp_path / "manifest.jsonl").write_text(json.dumps({"path": "s/sample.pt"}) + "\n")
+    sample = resolve_trace_sample(manifest_path=tmp_path / "manifest.jsonl")
+    p = load_trace_payload(sample)
+    sel = select_router_topk(p, layer=0, token_index=1, scores_to_weights=mode)
+    with RepackedMoeExpertStore(d) as store:
+        mlp = load_topk_expert_mlp(store, layer=0,
+                                   expert_ids=[int(v) for v in sel.expert_ids.tolist()], bits=4,
+                                   dtype=target, device="cuda")
+    x = select_trace_hidden_token(p, token_index=1).to(device="cuda", dtype=target)
+    w = sel.expert_weights.to(device=x.device, dtype=target)
+    with torch.inference_mode():
+        out = mlp(x, sel.expert_ids.to(torch.long), w)
+    assert out.shape == (1, 1, H) and out.dtype == target
+    assert bool(torch.isfinite(out).all().item())
+    xb = x.reshape(1, H).to(torch.bfloat16)
+    ref = moe_ref.moe_layer_f32(bf16_bits(xb), sel.expert_ids.numpy().astype(np.int32)[None],
+                                w.float().cpu().numpy()[None], experts_to_np(ex))
+    err = moe_ref.rel_err(out.reshape(1, H).float().cpu().numpy(), ref)
+    print(f"  trace {dtype_name}/{mode}: rel_err={err:.3e}", flush=True)
+    assert err <= LAYER_RTOL
