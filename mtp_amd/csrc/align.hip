@@ -86,10 +86,11 @@ __global__ __launch_bounds__(64) void align_chunk_kernel(const int32_t* __restri
 // gives each lane's first position. An expert's blocks are all full except the last.
 constexpr int kOrderMaxClasses = 8;  // BM <= 128
 // Subtiles holding slots in the last block of a group of n > 0 slots.
-MOE_DEV int last_class(int n, int BM) { return (n - (n - 1) / BM * BM + 15) / 16; }
+MOE_DEV int last_class(int n, const BlockDiv& bd) { return (n - bd.div(n - 1) * bd.bm + 15) / 16; }
 MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, int BM, int lane,
                          int32_t* __restrict__ border) {
   const int NC = BM / 16;
+  const BlockDiv bd(BM);
   const int per = (G + 63) / 64;
   const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
   int cnt[kOrderMaxClasses];  // cnt[c]: this lane's blocks of class c + 1
@@ -98,10 +99,10 @@ MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, int BM, int 
   for (int g = g0; g < g1; ++g) {
     const int n = s_cnt[g];
     if (n == 0) continue;
-    const int lc = last_class(n, BM);
+    const int lc = last_class(n, bd);
 #pragma unroll
     for (int c = 0; c < kOrderMaxClasses; ++c) {
-      if (c == NC - 1) cnt[c] += (n - 1) / BM;  // the full blocks before the last
+      if (c == NC - 1) cnt[c] += bd.div(n - 1);  // the full blocks before the last
       if (c == lc - 1) cnt[c] += 1;
     }
   }
@@ -109,18 +110,14 @@ MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, int BM, int 
   int base = 0;
 #pragma unroll
   for (int c = kOrderMaxClasses - 1; c >= 0; --c) {  // classes heaviest first
-    int incl = cnt[c];
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_sum(cnt[c]);
     pos[c] = base + incl - cnt[c];
-    base += __shfl(incl, 63, 64);
+    base += __builtin_amdgcn_readlane(incl, 63);
   }
   for (int g = g0; g < g1; ++g) {
     const int n = s_cnt[g];
     if (n == 0) continue;
-    const int b0 = s_off[g] / BM, nb = (n + BM - 1) / BM, lc = last_class(n, BM);
+    const int b0 = bd.div(s_off[g]), nb = bd.div(n + BM - 1), lc = last_class(n, bd);
 #pragma unroll
     for (int c = 0; c < kOrderMaxClasses; ++c) {
       if (c == NC - 1)
@@ -141,6 +138,7 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
   const int routed = T * top_k;
   const int n_slots = routed + (has_shared ? T : 0);
   const int G = E + (has_shared ? 1 : 0);
+  const BlockDiv bd(BM);
   // 1. everything this block reads from the scratch, before anything is written
   {  // 16 count loads per thread in flight together (buffer loads; past the end: zeros)
     constexpr int NL = (kAlign2LdsCounts + 1023) / 1024;
@@ -188,16 +186,12 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
     const int per = (G + 63) / 64;
     const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
     int local = 0;
-    for (int g = g0; g < g1; ++g) local += (s_pad[g] + BM - 1) / BM * BM;
-    int incl = local;
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    for (int g = g0; g < g1; ++g) local += bd.pad(s_pad[g]);
+    const int incl = wave_incl_sum(local);
     int run = incl - local;
     for (int g = g0; g < g1; ++g) {
       s_off[g] = run;
-      run += (s_pad[g] + BM - 1) / BM * BM;
+      run += bd.pad(s_pad[g]);
     }
     if (lane == 63) s_total = incl;
   }
@@ -220,9 +214,10 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
     }
     const i32x4 sent = {n_slots, n_slots, n_slots, n_slots};
     for (int p = a4 + 4 * sub; p < v_end; p += 16) *reinterpret_cast<i32x4*>(&sorted[p]) = sent;
-    for (int b = off / BM + sub; b < end / BM && b < cap; b += 4) eids[b] = g;
+    const int bend = min(bd.div(end), cap);
+    for (int b = bd.div(off) + sub; b < bend; b += 4) eids[b] = g;
   }
-  for (int b = tp / BM + tid; b < cap; b += 1024) eids[b] = -1;
+  for (int b = bd.div(tp) + tid; b < cap; b += 1024) eids[b] = -1;
   for (int p = tp + tid; p < limit; p += 1024) sorted[p] = n_slots;
   if (tid == 0) *ntpp = tp;
   // 5. the slots
@@ -258,6 +253,7 @@ __global__ __launch_bounds__(1024) void align_scatter_kernel(
   const int routed = T * top_k;
   const int n_slots = routed + (has_shared ? T : 0);
   const int G = E + (has_shared ? 1 : 0);
+  const BlockDiv bd(BM);
   const int ncnt = nchunks * G;
   // 1. all counts (16 loads per thread in flight together) and this thread's first slot of the
   //    chunk (its rank and raw id)
@@ -297,10 +293,11 @@ __global__ __launch_bounds__(1024) void align_scatter_kernel(
       tot += q < nchunks ? n : 0;
       pre += q < c ? n : 0;
     }
-    tot += __shfl_xor(tot, 1, 64);
-    pre += __shfl_xor(pre, 1, 64);
-    tot += __shfl_xor(tot, 2, 64);
-    pre += __shfl_xor(pre, 2, 64);
+    // quad sums through DPP: quad_perm(1,0,3,2) then quad_perm(2,3,0,1) (a quad is always whole)
+    tot += __builtin_amdgcn_update_dpp(0, tot, 0xB1, 0xF, 0xF, false);
+    pre += __builtin_amdgcn_update_dpp(0, pre, 0xB1, 0xF, 0xF, false);
+    tot += __builtin_amdgcn_update_dpp(0, tot, 0x4E, 0xF, 0xF, false);
+    pre += __builtin_amdgcn_update_dpp(0, pre, 0x4E, 0xF, 0xF, false);
     if (part == 0) {
       s_cnt[g] = tot;
       s_pre[g] = pre;
@@ -312,16 +309,12 @@ __global__ __launch_bounds__(1024) void align_scatter_kernel(
     const int per = (G + 63) / 64;
     const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
     int local = 0;
-    for (int g = g0; g < g1; ++g) local += (s_cnt[g] + BM - 1) / BM * BM;
-    int incl = local;
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    for (int g = g0; g < g1; ++g) local += bd.pad(s_cnt[g]);
+    const int incl = wave_incl_sum(local);
     int run = incl - local;
     for (int g = g0; g < g1; ++g) {
       s_off[g] = run;
-      run += (s_cnt[g] + BM - 1) / BM * BM;
+      run += bd.pad(s_cnt[g]);
     }
     if (lane == 63) s_total = incl;
   }
@@ -339,9 +332,10 @@ __global__ __launch_bounds__(1024) void align_scatter_kernel(
     const int off = s_off[g], real_end = off + s_cnt[g];
     const int end = min(g + 1 < G ? s_off[g + 1] : tp, limit);
     for (int p = real_end + tid; p < end; p += 1024) sorted[p] = n_slots;
-    for (int b = off / BM + tid; b < end / BM; b += 1024) eids[b] = g;
+    const int bend = bd.div(end);
+    for (int b = bd.div(off) + tid; b < bend; b += 1024) eids[b] = g;
   }
-  for (int b = tp / BM + c * 1024 + tid; b < cap; b += nchunks * 1024) eids[b] = -1;
+  for (int b = bd.div(tp) + c * 1024 + tid; b < cap; b += nchunks * 1024) eids[b] = -1;
   for (int p = tp + c * 1024 + tid; p < limit; p += nchunks * 1024) sorted[p] = n_slots;
   // 5. the slots of this chunk
   for (int f = f0; f < hi; f += 1024) {

@@ -137,7 +137,7 @@ struct StreamView {
   const int32_t* bq;          // packed row kq of step 0 at the lane's first column
   const uint16_t* bs;         // scales of group 0 at the lane's first column
   const int32_t* bz;          // zeros word of group 0 holding the lane's columns
-  int NOUT, G, nsteps, zsh;
+  int NOUT, gsh, nsteps, zsh;  // gsh: log2 of the group size
 
   // Step s of the ring; a prefetch past the last step re-reads the last step (in bounds; it is
   // never multiplied), so every pass issues the same loads.
@@ -146,7 +146,7 @@ struct StreamView {
     const int sc = min(s, nsteps - 1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int g = (sc * BK + 64 * h) / G;
+      const int g = (sc * BK + 64 * h) >> gsh;
       st.gz[h].s = *reinterpret_cast<const u32x2*>(bs + (int64_t)g * NOUT);
       st.gz[h].z = (uint32_t)bz[(int64_t)g * (NOUT / 8)];
     }
@@ -309,6 +309,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   const bool is_shared = (e == ed.num_experts);
   const int64_t row = is_shared ? 0 : expert_row(ed, e);
   const int K8 = K / 8, NG = K / G;
+  const int gsh = __builtin_ctz(G);  // group sizes are powers of two (64, 128, 256)
 
   if (tid < BM) {
     const int f = sorted[b * BM + tid];
@@ -358,7 +359,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
     v.bs = bs;
     v.bz = bz;
     v.NOUT = NOUT;
-    v.G = G;
+    v.gsh = gsh;
     v.nsteps = K / BK;
     v.zsh = zsh;
     // step count of the usual shapes (hidden 2048, intermediate 512): a straight-line ring
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   u32x4 bw[2][4];
   GroupSZ gz[2][2];
   auto load_gz = [&](int slot, int step, int h) {
-    const int g = (min(step, nsteps - 1) * BK + 64 * h) / G;
+    const int g = (min(step, nsteps - 1) * BK + 64 * h) >> gsh;
     gz[slot][h].s = *reinterpret_cast<const u32x2*>(bs + (int64_t)g * NOUT);
     gz[slot][h].z = (uint32_t)bz[(int64_t)g * (NOUT / 8)];
   };

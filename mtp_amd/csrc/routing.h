@@ -276,12 +276,14 @@ MOE_DEV void topk_select(const float* __restrict__ row, int E, int top_k, int la
   my_v = (lane < top_k) ? topk_ord_value(my_key) : 0.0f;
 }
 
-// Renormalised weight of lane r's selection: exp(l_r - l_0) / sum_{j < k} exp(l_j - l_0).
+// Renormalised weight of lane r's selection: exp(l_r - l_0) / sum_{j < k} exp(l_j - l_0), the sum
+// in selection order. Called by a whole wave (the lane reads are v_readlane, not LDS permutes).
 MOE_DEV float topk_weight(float my_v, int top_k, int lane) {
-  const float vmax = __shfl(my_v, 0, 64);
+  const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
   const float ex = (lane < top_k) ? expf(my_v - vmax) : 0.0f;
   float s = 0.0f;
-  for (int r = 0; r < top_k; ++r) s = s + __shfl(ex, r, 64);
+  for (int r = 0; r < top_k; ++r)
+    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
   return ex / s;
 }
 
@@ -350,6 +352,28 @@ struct AlignSmem {
   int total_padded;
 };
 
+// Inclusive prefix sum over the 64 lanes of a wave through DPP: row shifts by 1, 2, 4 and 8
+// (a lane whose source lies before its row keeps 0), then row_bcast15 into rows 1 and 3 and
+// row_bcast31 into rows 2 and 3. Six dependent VALU operations instead of six LDS permutes.
+MOE_DEV int wave_incl_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast31
+  return v;
+}
+
+// Division by the (wave-uniform) align block size for n >= 0: a shift when it is a power of two,
+// as the kernels' block sizes are, else an integer division (a uniform branch).
+struct BlockDiv {
+  int bm, sh;
+  MOE_DEV explicit BlockDiv(int b) : bm(b), sh((b & (b - 1)) == 0 ? __builtin_ctz(b) : -1) {}
+  MOE_DEV int div(int n) const { return sh >= 0 ? (n >> sh) : n / bm; }
+  MOE_DEV int pad(int n) const { return div(n + bm - 1) * bm; }  // n rounded up to blocks
+};
+
 MOE_DEV int slot_expert(const int32_t* topk_ids, int routed, int E, int f) {
   if (f < routed) {
     const int e = topk_ids[f];
@@ -389,6 +413,7 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
   const int routed = T * top_k;
   const int n_slots = routed + (has_shared ? T : 0);
   const int G = E + (has_shared ? 1 : 0);
+  const BlockDiv bd(BM);
   for (int i = tid; i < kAlignWaves * kMaxGroups; i += 1024) (&sm.cnt[0][0])[i] = 0;
   __syncthreads();
 
@@ -408,7 +433,7 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
   for (int g = tid; g < G; g += 1024) {
     int tot = 0;
     for (int v = 0; v < kAlignWaves; ++v) tot += sm.cnt[v][g];
-    sm.pad[g] = (tot + BM - 1) / BM * BM;
+    sm.pad[g] = bd.pad(tot);
   }
   __syncthreads();
   if (w == 0) {  // exclusive scan of pad[] by one wave: lane owns a contiguous run
@@ -416,11 +441,7 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
     const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
     int local = 0;
     for (int g = g0; g < g1; ++g) local += sm.pad[g];
-    int incl = local;
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_sum(local);
     int run = incl - local;
     for (int g = g0; g < g1; ++g) {
       sm.off[g] = run;
@@ -459,9 +480,10 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
     }
     const i32x4 sent = {n_slots, n_slots, n_slots, n_slots};
     for (int p = a4 + 4 * sub; p < v_end; p += 16) *reinterpret_cast<i32x4*>(&sorted[p]) = sent;
-    for (int b = off / BM + sub; b < end / BM && b < cap; b += 4) eids[b] = g;
+    const int bend = min(bd.div(end), cap);
+    for (int b = bd.div(off) + sub; b < bend; b += 4) eids[b] = g;
   }
-  for (int b = tp / BM + tid; b < cap; b += 1024) eids[b] = -1;
+  for (int b = bd.div(tp) + tid; b < cap; b += 1024) eids[b] = -1;
   for (int p = tp + tid; p < cap * BM; p += 1024) sorted[p] = n_slots;
   if (tid == 0) *ntpp = tp;
   __syncthreads();
@@ -527,7 +549,8 @@ MOE_DEV void align_wave(const int32_t* topk_ids, int T, int top_k, int E, int ha
   const int rank = __popcll(peers & lt_mask);
   const int cnt = __popcll(peers);
   const bool leader = valid && rank == 0;
-  const int padded = (cnt + BM - 1) / BM * BM;
+  const BlockDiv bd(BM);
+  const int padded = bd.pad(cnt);
 
   // padded sizes by group id, then an exclusive scan in place (lane owns a contiguous run)
   for (int g = lane; g < G; g += 64) pad_lds[g] = 0;
@@ -538,13 +561,8 @@ MOE_DEV void align_wave(const int32_t* topk_ids, int T, int top_k, int E, int ha
   const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
   int local = 0;
   for (int g = g0; g < g1; ++g) local += pad_lds[g];
-  int incl = local;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
-  const int total = __shfl(incl, 63, 64);
+  const int incl = wave_incl_sum(local);
+  const int total = __builtin_amdgcn_readlane(incl, 63);
   int run = incl - local;
   for (int g = g0; g < g1; ++g) {
     const int pg = pad_lds[g];
@@ -558,10 +576,11 @@ MOE_DEV void align_wave(const int32_t* topk_ids, int T, int top_k, int E, int ha
   if (valid && off + rank < limit) sorted[off + rank] = lane;
   if (leader) {
     for (int p = off + cnt; p < off + padded && p < limit; ++p) sorted[p] = n_slots;
-    for (int b = off / BM; b < (off + padded) / BM && b < cap; ++b) eids[b] = e;
+    const int b1 = min(bd.div(off + padded), cap);
+    for (int b = bd.div(off); b < b1; ++b) eids[b] = e;
   }
   if (fill_tail) {
-    for (int b = total / BM + lane; b < cap; b += 64) eids[b] = -1;
+    for (int b = bd.div(total) + lane; b < cap; b += 64) eids[b] = -1;
     for (int p = total + lane; p < limit; p += 64) sorted[p] = n_slots;
   }
   if (lane == 0) *ntpp = total;
