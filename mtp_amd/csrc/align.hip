@@ -82,48 +82,50 @@ __global__ __launch_bounds__(64) void align_chunk_kernel(const int32_t* __restri
 // Block order for the grouped GEMMs, heaviest first: border[r] = the r-th align block sorted by
 // its number of 16-row subtiles holding slots (class BM/16 first, down to 1), ties in block
 // order. Big blocks then start in the first wave of workgroups and the light ones fill the tail.
-// One wave: lane l owns groups [l per, (l + 1) per); per class, an exclusive scan over lanes
-// gives each lane's first position. An expert's blocks are all full except the last.
+// A group of n > 0 slots has (n - 1) / BM full blocks (class BM/16) and a last block of class
+// last_class(n); within a class the blocks come group by group, so with thread g taking group g
+// a block's position is its class's base plus an exclusive scan over the threads. Called by
+// every thread of a 1024-thread workgroup (it synchronises); wtot: 8 x 16 ints of LDS.
 constexpr int kOrderMaxClasses = 8;  // BM <= 128
 // Subtiles holding slots in the last block of a group of n > 0 slots.
 MOE_DEV int last_class(int n, const BlockDiv& bd) { return (n - bd.div(n - 1) * bd.bm + 15) / 16; }
-MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, int BM, int lane,
-                         int32_t* __restrict__ border) {
-  const int NC = BM / 16;
-  const BlockDiv bd(BM);
-  const int per = (G + 63) / 64;
-  const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
-  int cnt[kOrderMaxClasses];  // cnt[c]: this lane's blocks of class c + 1
+MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, const BlockDiv& bd,
+                         int (*wtot)[16], int32_t* __restrict__ border) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int NC = bd.bm / 16;
+  const int n = tid < G ? s_cnt[tid] : 0;
+  const int nfull = n > 0 ? bd.div(n - 1) : 0;
+  const int lc = n > 0 ? last_class(n, bd) : 0;  // 0: no blocks
+  const int b0 = tid < G ? bd.div(s_off[tid]) : 0;
+  int cnt[kOrderMaxClasses], excl[kOrderMaxClasses];
 #pragma unroll
-  for (int c = 0; c < kOrderMaxClasses; ++c) cnt[c] = 0;
-  for (int g = g0; g < g1; ++g) {
-    const int n = s_cnt[g];
-    if (n == 0) continue;
-    const int lc = last_class(n, bd);
-#pragma unroll
-    for (int c = 0; c < kOrderMaxClasses; ++c) {
-      if (c == NC - 1) cnt[c] += bd.div(n - 1);  // the full blocks before the last
-      if (c == lc - 1) cnt[c] += 1;
-    }
-  }
-  int pos[kOrderMaxClasses];  // this lane's next position per class
-  int base = 0;
-#pragma unroll
-  for (int c = kOrderMaxClasses - 1; c >= 0; --c) {  // classes heaviest first
+  for (int c = 0; c < kOrderMaxClasses; ++c) {
+    cnt[c] = (c == NC - 1 ? nfull : 0) + (c == lc - 1 ? 1 : 0);
     const int incl = wave_incl_sum(cnt[c]);
-    pos[c] = base + incl - cnt[c];
-    base += __builtin_amdgcn_readlane(incl, 63);
+    excl[c] = incl - cnt[c];
+    if (lane == 63) wtot[c][w] = incl;
   }
-  for (int g = g0; g < g1; ++g) {
-    const int n = s_cnt[g];
-    if (n == 0) continue;
-    const int b0 = bd.div(s_off[g]), nb = bd.div(n + BM - 1), lc = last_class(n, bd);
+  __syncthreads();
+  // positions: classes heaviest first, then the waves before this one, then the lanes
+  int base = 0, pos[kOrderMaxClasses];
 #pragma unroll
-    for (int c = 0; c < kOrderMaxClasses; ++c) {
-      if (c == NC - 1)
-        for (int j = 0; j < nb - 1; ++j) border[pos[c]++] = b0 + j;
-      if (c == lc - 1) border[pos[c]++] = b0 + nb - 1;
+  for (int c = kOrderMaxClasses - 1; c >= 0; --c) {
+    int tot = 0, before = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int v = wtot[c][i];
+      tot += v;
+      before += i < w ? v : 0;
     }
+    pos[c] = base + before + excl[c];
+    base += tot;
+  }
+  if (n > 0) {
+    for (int j = 0; j < nfull; ++j) border[pos[NC - 1] + j] = b0 + j;
+    int pl = 0;  // the last block's position (after this group's full blocks in class BM/16)
+#pragma unroll
+    for (int c = 0; c < kOrderMaxClasses; ++c) pl = c == lc - 1 ? pos[c] : pl;
+    border[pl + (lc == NC ? nfull : 0)] = b0 + nfull;
   }
 }
 
@@ -133,7 +135,7 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
     int32_t* __restrict__ ntpp, int32_t* __restrict__ border) {
   __shared__ int cl[kAlign2LdsCounts];  // [chunk][group]: counts, then bases inside the group
   __shared__ int s_off[kMaxGroups], s_pad[kMaxGroups];
-  __shared__ int s_total;
+  __shared__ int s_wtot[kOrderMaxClasses][16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int routed = T * top_k;
   const int n_slots = routed + (has_shared ? T : 0);
@@ -181,24 +183,15 @@ __global__ __launch_bounds__(1024) void align_finish_kernel(
     s_pad[g] = run;  // the group's slot count for now
   }
   __syncthreads();
-  // 3. group offsets: exclusive scan of the padded sizes by one wave
-  if (w == 0) {
-    const int per = (G + 63) / 64;
-    const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
-    int local = 0;
-    for (int g = g0; g < g1; ++g) local += bd.pad(s_pad[g]);
-    const int incl = wave_incl_sum(local);
-    int run = incl - local;
-    for (int g = g0; g < g1; ++g) {
-      s_off[g] = run;
-      run += bd.pad(s_pad[g]);
-    }
-    if (lane == 63) s_total = incl;
+  // 3. group offsets: exclusive scan of the padded sizes over the groups (thread g: group g)
+  int tp;
+  {
+    const int off = block_excl_sum(tid < G ? bd.pad(s_pad[tid]) : 0, s_wtot[0], tp);
+    if (tid < G) s_off[tid] = off;
   }
   __syncthreads();
-  const int tp = s_total;
   const int limit = cap * BM;
-  if (border && w == 0) block_order(s_off, s_pad, G, BM, lane, border);
+  if (border) block_order(s_off, s_pad, G, bd, s_wtot, border);
   // 4. padding sentinels (four threads per group, 16-byte stores) and block ids
   const bool vec = (reinterpret_cast<uintptr_t>(sorted) & 15u) == 0;
   for (int g = tid >> 2; g < G; g += 256) {
@@ -248,7 +241,7 @@ __global__ __launch_bounds__(1024) void align_scatter_kernel(
     int32_t* __restrict__ border) {
   __shared__ int cl[kAlign2LdsCounts];  // [chunk][group] counts
   __shared__ int s_off[kMaxGroups], s_cnt[kMaxGroups], s_pre[kMaxGroups];
-  __shared__ int s_total;
+  __shared__ int s_wtot[kOrderMaxClasses][16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = blockIdx.x;
   const int routed = T * top_k;
   const int n_slots = routed + (has_shared ? T : 0);
@@ -304,28 +297,19 @@ __global__ __launch_bounds__(1024) void align_scatter_kernel(
     }
   }
   __syncthreads();
-  // 3. group offsets: exclusive scan of the padded sizes by one wave
-  if (w == 0) {
-    const int per = (G + 63) / 64;
-    const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
-    int local = 0;
-    for (int g = g0; g < g1; ++g) local += bd.pad(s_cnt[g]);
-    const int incl = wave_incl_sum(local);
-    int run = incl - local;
-    for (int g = g0; g < g1; ++g) {
-      s_off[g] = run;
-      run += bd.pad(s_cnt[g]);
-    }
-    if (lane == 63) s_total = incl;
+  // 3. group offsets: exclusive scan of the padded sizes over the groups (thread g: group g)
+  int tp;
+  {
+    const int off = block_excl_sum(tid < G ? bd.pad(s_cnt[tid]) : 0, s_wtot[0], tp);
+    if (tid < G) s_off[tid] = off;
   }
   __syncthreads();
-  const int tp = s_total;
   const int limit = cap * BM;
   // 4. this workgroup's share of the layout: groups c, c + nchunks, ... (padding sentinels and
   //    block ids), a stride of the tail past the padded total, ntpp and the block order
   if (c == nchunks) {  // the extra workgroup: ntpp and the block order only
     if (tid == 0) *ntpp = tp;
-    if (border && w == 0) block_order(s_off, s_cnt, G, BM, lane, border);
+    if (border) block_order(s_off, s_cnt, G, bd, s_wtot, border);
     return;
   }
   for (int g = c; g < G; g += nchunks) {

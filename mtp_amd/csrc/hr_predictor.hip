@@ -29,8 +29,7 @@ constexpr int kCtxMaxPerThread = 4;  // width <= 1024
 
 // Fixed-order sum over the workgroup: per-thread value -> wave butterfly -> waves in order.
 MOE_DEV float block_sum(float v, float* red) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  v = bfly_sum(v);
   const int wv = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[wv] = v;

@@ -60,8 +60,7 @@ MOE_DEV void norm_rows(const uint16_t* const (&res_in)[TT], const uint16_t* cons
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss[i] = __builtin_fmaf(v[i][c][e], v[i][c][e], ss[i]);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) ss[i] = wave_xor_sum(ss[i], m);
+    ss[i] = bfly_sum(ss[i]);
     if (lane == 0) s_part[4 * i + wave] = ss[i];
   }
   __syncthreads();

@@ -133,8 +133,8 @@ __global__ __launch_bounds__(64 * kKSplit) void router_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v = n2[j];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+      v += xor_partner<16>(v);
+      v += xor_partner<32>(v);
       s_n2[wv][j][lane] = v;
     }
   }
@@ -163,57 +163,6 @@ __global__ __launch_bounds__(64 * kKSplit) void router_mfma_kernel(
       if (kq == 0 && e < E) nw2[e] = v;
     }
   }
-}
-
-// Lane i receives lane (i ^ M)'s value, through DPP and cross-row permutes rather than LDS
-// (ds_bpermute). A butterfly v = v + xor_partner<M>(v) over M = 32 .. 1 adds the same two
-// operands at every lane as v += shfl_xor(v, M) (fp32 addition is commutative), so sums are
-// bit-identical to the canonical order's butterfly.
-template <int M>
-MOE_DEV float xor_partner(float v) {
-  const int iv = __float_as_int(v);
-  if constexpr (M == 32) {
-    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)iv, (uint32_t)iv, false, false);
-    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-  } else if constexpr (M == 16) {
-    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)iv, (uint32_t)iv, false, false);
-    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
-  } else if constexpr (M == 8) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false));  // row_ror:8
-  } else if constexpr (M == 4) {  // half-row mirror (i -> 7 - i), then quad reverse: i -> i ^ 4
-    const int m = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, false);
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false));
-  } else if constexpr (M == 2) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
-  } else {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
-  }
-}
-
-MOE_DEV float bfly_sum(float v) {
-  v = v + xor_partner<32>(v);
-  v = v + xor_partner<16>(v);
-  v = v + xor_partner<8>(v);
-  v = v + xor_partner<4>(v);
-  v = v + xor_partner<2>(v);
-  v = v + xor_partner<1>(v);
-  return v;
-}
-MOE_DEV float bfly_min(float v) {
-  v = fminf(v, xor_partner<32>(v));
-  v = fminf(v, xor_partner<16>(v));
-  v = fminf(v, xor_partner<8>(v));
-  v = fminf(v, xor_partner<4>(v));
-  v = fminf(v, xor_partner<2>(v));
-  return fminf(v, xor_partner<1>(v));
-}
-MOE_DEV float bfly_max(float v) {
-  v = fmaxf(v, xor_partner<32>(v));
-  v = fmaxf(v, xor_partner<16>(v));
-  v = fmaxf(v, xor_partner<8>(v));
-  v = fmaxf(v, xor_partner<4>(v));
-  v = fmaxf(v, xor_partner<2>(v));
-  return fmaxf(v, xor_partner<1>(v));
 }
 
 constexpr int kCertWaves = 4;

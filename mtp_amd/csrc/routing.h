@@ -82,12 +82,7 @@ MOE_DEV void logits_tile(const uint16_t* __restrict__ x, int T, int H, const uin
 #pragma unroll
     for (int j = 0; j < TE; ++j) {
       float v = acc[i][j];
-      v = wave_xor_sum(v, 32);
-      v = wave_xor_sum(v, 16);
-      v = wave_xor_sum(v, 8);
-      v = wave_xor_sum(v, 4);
-      v = wave_xor_sum(v, 2);
-      v = wave_xor_sum(v, 1);
+      v = bfly_sum(v);
       acc[i][j] = v;
     }
   if (lane == 0) {
@@ -169,12 +164,7 @@ struct LdsLogitsTile {
 #pragma unroll
       for (int j = 0; j < TE; ++j) {
         float v = acc[i][j];
-        v = wave_xor_sum(v, 32);
-        v = wave_xor_sum(v, 16);
-        v = wave_xor_sum(v, 8);
-        v = wave_xor_sum(v, 4);
-        v = wave_xor_sum(v, 2);
-        v = wave_xor_sum(v, 1);
+        v = bfly_sum(v);
         acc[i][j] = v;
       }
     if (lane == 0) {
@@ -349,7 +339,7 @@ struct AlignSmem {
   int cnt[kAlignWaves][kMaxGroups];
   int off[kMaxGroups];
   int pad[kMaxGroups];
-  int total_padded;
+  int wtot[16];
 };
 
 // Inclusive prefix sum over the 64 lanes of a wave through DPP: row shifts by 1, 2, 4 and 8
@@ -363,6 +353,25 @@ MOE_DEV int wave_incl_sum(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast15
   v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast31
   return v;
+}
+
+// Exclusive prefix sum of v over the threads of a workgroup of at most 16 waves, in thread order,
+// and the total. wtot: 16 ints of LDS. Every thread of the workgroup calls it (it synchronises);
+// wtot may be reused only after a further barrier.
+MOE_DEV int block_excl_sum(int v, int* wtot, int& total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nw = (blockDim.x + 63) >> 6;
+  const int incl = wave_incl_sum(v);
+  if (lane == 63) wtot[w] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = i < nw ? wtot[i] : 0;
+    tot += t;
+    before += i < w ? t : 0;
+  }
+  total = tot;
+  return before + incl - v;
 }
 
 // Division by the (wave-uniform) align block size for n >= 0: a shift when it is a power of two,
@@ -430,27 +439,17 @@ MOE_DEV void align_block(const int32_t* topk_ids, int T, int top_k, int E, int h
     }
   }
   __syncthreads();
-  for (int g = tid; g < G; g += 1024) {
+  int tp;
+  {  // padded group sizes and their exclusive scan over the groups (thread g: group g)
     int tot = 0;
-    for (int v = 0; v < kAlignWaves; ++v) tot += sm.cnt[v][g];
-    sm.pad[g] = bd.pad(tot);
+    if (tid < G)
+      for (int v = 0; v < kAlignWaves; ++v) tot += sm.cnt[v][tid];
+    const int pad = bd.pad(tot);
+    if (tid < G) sm.pad[tid] = pad;
+    const int off = block_excl_sum(pad, sm.wtot, tp);
+    if (tid < G) sm.off[tid] = off;
   }
   __syncthreads();
-  if (w == 0) {  // exclusive scan of pad[] by one wave: lane owns a contiguous run
-    const int per = (G + 63) / 64;
-    const int g0 = min(lane * per, G), g1 = min(g0 + per, G);
-    int local = 0;
-    for (int g = g0; g < g1; ++g) local += sm.pad[g];
-    const int incl = wave_incl_sum(local);
-    int run = incl - local;
-    for (int g = g0; g < g1; ++g) {
-      sm.off[g] = run;
-      run += sm.pad[g];
-    }
-    if (lane == 63) sm.total_padded = incl;
-  }
-  __syncthreads();
-  const int tp = sm.total_padded;
   // Bases: one thread per group turns the 16 waves' counts into running offsets (all groups in
   // parallel) and leaves the end of the group's real slots in pad[]. Then four threads per group
   // write its padding sentinels with 16-byte stores (scalar stores for an unaligned head or tail)
