@@ -1,6 +1,8 @@
 // Prefill path: grouped bf16 MFMA GEMMs over block-padded expert groups, with the int4 weights
-// dequantised exactly in registers (reference dequant semantics, bit-exact bf16), fused
-// SiLU*mul (W1) and routed-weight (W2) epilogues.
+// dequantised in registers, fused SiLU*mul (W1) and routed-weight (W2) epilogues. Blocks of more
+// than two 16-row subtiles dequantise exactly (reference dequant semantics, bit-exact bf16
+// weights); lighter blocks fold the zero point and scale into the per-group MFMA sums (the decode
+// kernels' arithmetic: weights unrounded, layer outputs within the same tolerance).
 //
 // Arithmetic follows src/mtp_expert_prefetch/tracing/vllm_wna16_group_plan.py:367-486
 // (A row = slot // top_k, b = ((q - z) * s).to(bf16), fp32 accumulation) and the expert MLP of
@@ -22,7 +24,10 @@
 //   W2: 64 output columns of the hidden dimension; epilogue writes w[slot] * acc (fp32 or bf16).
 // 16-row subtiles that hold only padding are neither loaded nor multiplied. Blocks with at most
 // two subtiles of slots (experts with few tokens) take a streaming path instead: no LDS, a
-// register ring several k-steps deep (see stream_block).
+// register ring several k-steps deep, folded dequant (see stream_block). There the exact
+// dequant's ~19 VALU operations per packed word cost more than the multiplications they feed;
+// the fold needs 7 per word plus two per output element and group (measured: prefill-2048
+// 259 -> 248 us per layer).
 #include <type_traits>
 
 #include "common.h"
@@ -50,11 +55,12 @@ MOE_DEV void buf_ld128_lds(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t off
 }
 
 // Streaming path: blocks of at most kStreamMaxTiles row subtiles; ring depth (k-steps in
-// flight per wave) for one and for two subtiles. K is a multiple of 256, so the step count is
-// even (the runtime-count ring is 2 deep).
+// flight per wave) for one and for two subtiles (with the group sums of the fold, a 3-deep ring
+// for two subtiles spills). K is a multiple of 256, so the step count is even (the
+// runtime-count ring is 2 deep).
 constexpr int kStreamMaxTiles = 2;
 constexpr int kStreamDepth1 = 4;
-constexpr int kStreamDepth2 = 3;
+constexpr int kStreamDepth2 = 2;
 
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
@@ -66,6 +72,29 @@ enum { MODE_W1 = 1, MODE_W2 = 2 };
 MOE_DEV uint32_t pk_bf16(float lo, float hi) {
   bf16x2_t p = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, p);
+}
+
+// Folded dequant (light blocks): B fragments hold the exact bf16 values 128 + q, in the k order
+// [0,2,4,6,1,3,5,7] (two nibble byte planes, one byte permute per bf16 pair with the exponent
+// byte 0x43), and the A fragments are permuted to the same order; per quantisation group the
+// MFMA sums S = sum_k x (128 + q) and X = sum_k x (an all-ones B) are folded into the result as
+// s (S - (128 + z) X).
+constexpr uint32_t kFoldMagic = 0x43434343u;
+constexpr uint32_t kFoldOnes = 0x3F803F80u;  // bf16 pair (1, 1)
+MOE_DEV bf16x8_v fold_weight_frag(uint32_t w) {
+  const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+  const u32x4 o = {__builtin_amdgcn_perm(ev, kFoldMagic, 0x00050004u),
+                   __builtin_amdgcn_perm(ev, kFoldMagic, 0x00070006u),
+                   __builtin_amdgcn_perm(od, kFoldMagic, 0x00050004u),
+                   __builtin_amdgcn_perm(od, kFoldMagic, 0x00070006u)};
+  return __builtin_bit_cast(bf16x8_v, o);
+}
+MOE_DEV bf16x8_v fold_act_frag(const u32x4 d) {
+  const u32x4 o = {__builtin_amdgcn_perm(d[1], d[0], 0x05040100u),
+                   __builtin_amdgcn_perm(d[3], d[2], 0x05040100u),
+                   __builtin_amdgcn_perm(d[1], d[0], 0x07060302u),
+                   __builtin_amdgcn_perm(d[3], d[2], 0x07060302u)};
+  return __builtin_bit_cast(bf16x8_v, o);
 }
 
 // Exact bf16((q - z) * s) of the 8 nibbles of w (nibble j = k0 + j) as an MFMA B fragment.
@@ -121,7 +150,7 @@ MOE_DEV void static_for(F&& f) {
 // full round trip. Here each wave keeps D k-steps in flight in registers - the A fragments of
 // its MT row subtiles, the packed weight words and the step's scales and zeros, all buffer loads
 // (steps past K read zeros without a memory access) - and uses no LDS and no barrier. The
-// arithmetic (exact dequant, MFMA order over k) is the LDS path's.
+// dequant is the folded one (compute_fold).
 template <int MT>
 struct StreamStage {
   u32x4 a[MT][4];  // row mi*16 + j, 8 consecutive bf16 at k = 32 kk + 8 kq
@@ -160,22 +189,49 @@ struct StreamView {
       for (int kk = 0; kk < 4; ++kk) st.a[mi][kk] = buf_ld128(ar, a_off[mi] + ka + 64u * kk);
   }
 
+  // Folded form of compute for step `step`: group sums in gs / gx, folded into acc at the end of
+  // each quantisation group (group sizes >= 64, so a group ends at a half-step boundary).
   template <int MT>
-  MOE_DEV void compute(const StreamStage<MT>& st, f32x4 (&acc)[MT][4]) const {
-    _Float16 sc[4];
-    float cc[4];
+  MOE_DEV void compute_fold(const StreamStage<MT>& st, int step, f32x4 (&acc)[MT][4],
+                            f32x4 (&gs)[MT][4], f32x4 (&gx)[MT]) const {
+    const bf16x8_v ones =
+        __builtin_bit_cast(bf16x8_v, u32x4{kFoldOnes, kFoldOnes, kFoldOnes, kFoldOnes});
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      if ((kk & 1) == 0) group_coeffs(st.gz[kk >> 1], zsh, sc, cc);
-      bf16x8_v bfr[4];
-#pragma unroll
-      for (int n = 0; n < 4; ++n) bfr[n] = dequant8_exact(st.bw[kk][n], sc[n], cc[n]);
+      bf16x8_v af[MT];
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi) {
-        const bf16x8_v af = __builtin_bit_cast(bf16x8_v, st.a[mi][kk]);
+        af[mi] = fold_act_frag(st.a[mi][kk]);
+        gx[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], ones, gx[mi], 0, 0, 0);
+      }
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
-          acc[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[n], acc[mi][n], 0, 0, 0);
+      for (int n = 0; n < 4; ++n) {
+        const bf16x8_v wf = fold_weight_frag(st.bw[kk][n]);
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi)
+          gs[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], wf, gs[mi][n], 0, 0, 0);
+      }
+      if ((kk & 1) && (((step * BK + 32 * (kk + 1)) & ((1 << gsh) - 1)) == 0)) {  // group end
+        const GroupSZ& q = st.gz[kk >> 1];
+        const uint32_t zw = q.z >> zsh;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const float s =
+              (float)__builtin_bit_cast(_Float16, (uint16_t)(q.s[n >> 1] >> (16 * (n & 1))));
+          const float zb = 128.0f + (float)((zw >> (4 * n)) & 0xFu);
+#pragma unroll
+          for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[mi][n][i] =
+                  __builtin_fmaf(s, __builtin_fmaf(-zb, gx[mi][i], gs[mi][n][i]), acc[mi][n][i]);
+        }
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) {
+          gx[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int n = 0; n < 4; ++n) gs[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
   }
@@ -189,6 +245,13 @@ struct StreamView {
 template <int MT, int D, int NS>
 MOE_DEV void stream_block(const StreamView& v, f32x4 (&acc)[MT][4]) {
   StreamStage<MT> ring[D];
+  f32x4 gs[MT][4], gx[MT];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    gx[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) gs[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   static_for<0, D - 1>([&](auto jc) {
     v.load(ring[jc.value], jc.value);
     __builtin_amdgcn_sched_barrier(0);  // issue order = step order
@@ -198,7 +261,7 @@ MOE_DEV void stream_block(const StreamView& v, f32x4 (&acc)[MT][4]) {
       constexpr int st = sc.value;
       if constexpr (st + D - 1 < NS) v.load(ring[(st + D - 1) % D], st + D - 1);
       __builtin_amdgcn_sched_barrier(0);  // this stage's loads ahead of the wait for step st
-      v.compute(ring[st % D], acc);
+      v.compute_fold(ring[st % D], st, acc, gs, gx);
     });
   } else {
     for (int s0 = 0; s0 < v.nsteps; s0 += D) {
@@ -206,7 +269,7 @@ MOE_DEV void stream_block(const StreamView& v, f32x4 (&acc)[MT][4]) {
         constexpr int jj = jc.value;
         v.load(ring[(jj + D - 1) % D], s0 + jj + D - 1);
         __builtin_amdgcn_sched_barrier(0);
-        v.compute(ring[jj], acc);
+        v.compute_fold(ring[jj], s0 + jj, acc, gs, gx);
       });
     }
   }
