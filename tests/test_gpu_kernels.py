@@ -103,7 +103,12 @@ def test_router_ties_break_to_lower_id():
                                                   (2048, 8, 256, 128, False, True),
                                                   (2048, 8, 256, 128, True, False),
                                                   (33, 4, 16, 128, True, False),
-                                                  (1, 3, 8, 4, False, False)])
+                                                  (1, 3, 8, 4, False, False),
+                                                  # block sizes that are not powers of two
+                                                  # (the kernels' division fallback)
+                                                  (40, 8, 64, 24, False, False),
+                                                  (5, 3, 16, 12, True, False),
+                                                  (2048, 8, 256, 96, False, True)])
 def test_align_bit_exact(T, k, E, BM, shared, zipf):
     _say(f"align T={T} k={k} E={E} BM={BM} shared={shared} zipf={zipf}")
     rng = np.random.default_rng(T + BM)
