@@ -335,8 +335,17 @@ def main() -> int:
             "experts_with_zero_tokens": int((counts == 0).sum()),
         }
         prefill["mfma_frac"] = prefill["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
+        # HBM co-bound: the routed experts' bytes (each read at least once) over the same time;
+        # the router's FLOPs are reported apart from the useful expert FLOPs
+        u = int((counts > 0).sum())
+        prefill["expert_bytes"] = u * synth.expert_bytes()
+        prefill["GBps"] = prefill["expert_bytes"] / (med * 1e-3) / 1e9
+        prefill["hbm_frac"] = prefill["GBps"] / HBM_PEAK_GBPS
+        prefill["router_flop"] = 2 * Tp * E * H
         log(f"[bench] prefill T={Tp}: {med * 1e3:.1f} us/layer, {prefill['TFLOPs']:.1f} TFLOP/s "
-            f"({100 * prefill['mfma_frac']:.1f}% of bf16 MFMA peak)")
+            f"({100 * prefill['mfma_frac']:.1f}% of bf16 MFMA peak); expert bytes "
+            f"{prefill['expert_bytes'] / 1e6:.1f} MB at {prefill['GBps']:.0f} GB/s "
+            f"({100 * prefill['hbm_frac']:.1f}% of 8 TB/s)")
 
     # ------------------------------------------------------- full block with shared expert
     block = {}
