@@ -45,6 +45,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=40)
     p.add_argument("--batches", default="1,8,32,64")
     p.add_argument("--prefill-tokens", type=int, default=2048)
+    p.add_argument("--prefill-layers", type=int, default=8,
+                   help="resident layers chained in the prefill graph (per-layer time: replay / "
+                        "layers)")
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="wall-clock budget of the CPU baseline sample (0 disables it)")
     p.add_argument("--block-batches", default="1,32",
@@ -305,29 +308,48 @@ def main() -> int:
             f"p95 {buckets['w2_us']['p95']:.2f}")
 
     # ------------------------------------------------------------------ prefill-2048
+    # A chain of the first `prefill_layers` resident layers in one graph (as the decode chains),
+    # per-layer time = replay / layers; layer 0 alone per replay is reported beside it.
     Tp = args.prefill_tokens
     prefill = {}
     if Tp > 0:
-        ly = layers[0]
+        NLp = max(1, min(args.prefill_layers, len(layers)))
         xp = synth.make_tokens(Tp, seed=7, device=dev)
-        need = ops.workspace_bytes(Tp, K, ly.experts, False, "auto")
-        wsp = torch.zeros(need, dtype=torch.uint8, device=dev)
-        outp = torch.empty(Tp, H, dtype=torch.bfloat16, device=dev)
-        _, ids, _ = ops.moe_layer(xp, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
-                                  workspace=wsp, out=outp, return_routing=True)
-        counts = torch.bincount(ids.view(-1).long(), minlength=E)
-        gp = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gp):
-            ops.moe_layer(xp, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
-                          workspace=wsp, out=outp)
-        for _ in range(args.warmup):
-            gp.replay()
-        ts = median_event_ms(gp.replay, args.steps, stream)
-        med = statistics.median(ts)
+        wsps, outps, us = [], [], []
+        counts = None
+        for ly in layers[:NLp]:
+            need = ops.workspace_bytes(Tp, K, ly.experts, False, "auto")
+            wsps.append(torch.zeros(need, dtype=torch.uint8, device=dev))
+            outps.append(torch.empty(Tp, H, dtype=torch.bfloat16, device=dev))
+            _, ids, _ = ops.moe_layer(xp, ly.router_w, ly.experts, top_k=K,
+                                      logit_bias=ly.logit_bias, workspace=wsps[-1],
+                                      out=outps[-1], return_routing=True)
+            c = torch.bincount(ids.view(-1).long(), minlength=E)
+            counts = c if counts is None else counts
+            us.append(int((c > 0).sum()))
+
+        def prefill_chain(n):
+            for i in range(n):
+                ly = layers[i]
+                ops.moe_layer(xp, ly.router_w, ly.experts, top_k=K, logit_bias=ly.logit_bias,
+                              workspace=wsps[i], out=outps[i])
+
+        def replay_ms(n):
+            gp = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gp):
+                prefill_chain(n)
+            for _ in range(args.warmup):
+                gp.replay()
+            return statistics.median(median_event_ms(gp.replay, args.steps, stream)) / n
+
+        med = replay_ms(NLp)
+        single = replay_ms(1) if NLp > 1 else med
         flops = synth.prefill_flops(Tp)
         prefill = {
             "tokens": Tp,
+            "layers_in_chain": NLp,
             "layer_us_p50": med * 1e3,
+            "single_layer_us_p50": single * 1e3,
             "TFLOPs": flops / (med * 1e-3) / 1e12,
             "flop": flops,
             "expert_tokens_max": int(counts.max()),
@@ -337,12 +359,12 @@ def main() -> int:
         prefill["mfma_frac"] = prefill["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
         # HBM co-bound: the routed experts' bytes (each read at least once) over the same time;
         # the router's FLOPs are reported apart from the useful expert FLOPs
-        u = int((counts > 0).sum())
-        prefill["expert_bytes"] = u * synth.expert_bytes()
+        prefill["expert_bytes"] = statistics.mean(us) * synth.expert_bytes()
         prefill["GBps"] = prefill["expert_bytes"] / (med * 1e-3) / 1e9
         prefill["hbm_frac"] = prefill["GBps"] / HBM_PEAK_GBPS
         prefill["router_flop"] = 2 * Tp * E * H
-        log(f"[bench] prefill T={Tp}: {med * 1e3:.1f} us/layer, {prefill['TFLOPs']:.1f} TFLOP/s "
+        log(f"[bench] prefill T={Tp}: {med * 1e3:.1f} us/layer over {NLp} chained layers "
+            f"(layer 0 alone per replay {single * 1e3:.1f} us), {prefill['TFLOPs']:.1f} TFLOP/s "
             f"({100 * prefill['mfma_frac']:.1f}% of bf16 MFMA peak); expert bytes "
             f"{prefill['expert_bytes'] / 1e6:.1f} MB at {prefill['GBps']:.0f} GB/s "
             f"({100 * prefill['hbm_frac']:.1f}% of 8 TB/s)")
