@@ -93,7 +93,10 @@ MOE_DEV u32x4 ld128_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-MOE_DEV float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+// SiLU of the GEMM epilogues: g * (1 / (1 + e^-g)) with the hardware reciprocal (v_rcp_f32, 1 ulp)
+// instead of the IEEE division sequence: about 5 VALU operations instead of 15, and the product is
+// rounded to bf16 right after. (The predictors, whose activations feed a top-k, keep a division.)
+MOE_DEV float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // Device view of one projection of an expert set.
 struct ProjDev {
