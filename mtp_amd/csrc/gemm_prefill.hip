@@ -285,35 +285,45 @@ MOE_DEV void block_epilogue(const f32x4 (&acc)[M][4], int mtiles, const int* s_s
 #pragma unroll
   for (int mi = 0; mi < M; ++mi) {
     if (mi >= mtiles) break;
+    if constexpr (MODE == MODE_W1) {
+      // Lanes jj < 8 hold gate and lane jj + 8 the up value of the same column; a row rotation
+      // by 8 (row_ror:8) brings each its partner's. Rows are taken in pairs (el, el + 1): lanes
+      // jj < 8 form h of row el, lanes jj >= 8 h of row el + 1 from the gate value of lane
+      // jj - 8, so every lane computes one SiLU per pair of rows.
+      const bool lo = j < 8;
 #pragma unroll
-    for (int el = 0; el < 4; ++el) {
-      const int r = mi * 16 + 4 * kq + el;
-      const int f = s_slot[r];
-      if (MODE == MODE_W1) {
+      for (int el = 0; el < 4; el += 2) {
+        const int f = s_slot[mi * 16 + 4 * kq + el + (lo ? 0 : 1)];
         float hv[4];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          const float g = acc[mi][n][el];
-          // lanes jj < 8 hold gate, lane jj + 8 the up value of the same column (row_ror:8)
-          const float u = __int_as_float(
-              __builtin_amdgcn_update_dpp(0, __float_as_int(g), 0x128, 0xF, 0xF, false));
-          hv[n] = silu_f32(g) * u;
+          const float ga = acc[mi][n][el], gb = acc[mi][n][el + 1];
+          const float ra = __int_as_float(
+              __builtin_amdgcn_update_dpp(0, __float_as_int(ga), 0x128, 0xF, 0xF, false));
+          const float rb = __int_as_float(
+              __builtin_amdgcn_update_dpp(0, __float_as_int(gb), 0x128, 0xF, 0xF, false));
+          hv[n] = silu_f32(lo ? ga : rb) * (lo ? ra : gb);
         }
-        if (j < 8 && (unsigned)f < (unsigned)num_slots) {
+        if ((unsigned)f < (unsigned)num_slots) {
           const u32x2 o = {pk_bf16(hv[0], hv[1]), pk_bf16(hv[2], hv[3])};
           *reinterpret_cast<u32x2*>(&h_out[(int64_t)f * I + col]) = o;
         }
-      } else {
-        if ((unsigned)f < (unsigned)num_slots) {
-          const float w = s_w[r];
-          const f32x4 o = {w * acc[mi][0][el], w * acc[mi][1][el], w * acc[mi][2][el],
-                           w * acc[mi][3][el]};
-          if constexpr (YS16) {
-            const u32x2 ob = {pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3])};
-            *reinterpret_cast<u32x2*>(&static_cast<uint16_t*>(ys)[(int64_t)f * H + col]) = ob;
-          } else {
-            *reinterpret_cast<f32x4*>(&static_cast<float*>(ys)[(int64_t)f * H + col]) = o;
-          }
+      }
+      continue;
+    }
+#pragma unroll
+    for (int el = 0; el < 4; ++el) {  // W2: the routed weight times the row
+      const int r = mi * 16 + 4 * kq + el;
+      const int f = s_slot[r];
+      if ((unsigned)f < (unsigned)num_slots) {
+        const float w = s_w[r];
+        const f32x4 o = {w * acc[mi][0][el], w * acc[mi][1][el], w * acc[mi][2][el],
+                         w * acc[mi][3][el]};
+        if constexpr (YS16) {
+          const u32x2 ob = {pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3])};
+          *reinterpret_cast<u32x2*>(&static_cast<uint16_t*>(ys)[(int64_t)f * H + col]) = ob;
+        } else {
+          *reinterpret_cast<f32x4*>(&static_cast<float*>(ys)[(int64_t)f * H + col]) = o;
         }
       }
     }
