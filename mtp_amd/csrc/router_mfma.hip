@@ -113,8 +113,14 @@ __global__ __launch_bounds__(64 * kKSplit) void router_mfma_kernel(
         }
     }
   };
+  // The ring's first stages issued in step order, so that the wait before each step of the loop
+  // is for that step's stage only, on the first entry as on the back-edge (scheduled freely,
+  // slot 0's loads went out last and the wait at the loop head drained all but the newest stage).
 #pragma unroll
-  for (int j = 0; j < kMfmaRing - 1; ++j) load(j, j);
+  for (int j = 0; j < kMfmaRing - 1; ++j) {
+    load(j, j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   for (int s0 = 0; s0 < steps; s0 += kMfmaRing) {
 #pragma unroll
     for (int j = 0; j < kMfmaRing; ++j) {
