@@ -88,6 +88,19 @@ MOE_DEV uint32_t buf_ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
 }
 
+// s_waitcnt immediate waiting for vmcnt <= n only (expcnt and lgkmcnt at their maximum).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Buffer load of 16 bytes per lane straight into LDS: lane i writes lds[16 i, 16 i + 16) (bytes;
+// lds wave-uniform). An out-of-range offset writes zeros. The load counts in vmcnt until the
+// bytes are in LDS. (A device function: the builtin inside a lambda of a kernel makes the host
+// pass drop the kernel's launch stub.)
+MOE_DEV void buf_ld128_lds(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, off, 0, 0, 0);
+}
+
 MOE_DEV u32x4 ld128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 MOE_DEV u32x4 ld128_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

@@ -42,17 +42,6 @@ constexpr int kMTiles = BM / 16;    // 8 row subtiles
 // the count the wait for a step's A tile leaves in flight.
 constexpr int kLoadsPerStepB = 8;
 
-// s_waitcnt immediate waiting for vmcnt <= n only (expcnt and lgkmcnt at their maximum).
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// Buffer load of 16 bytes per lane straight into LDS: lane i writes lds[16 i, 16 i + 16) (bytes;
-// lds wave-uniform). An out-of-range offset writes zeros. (A device function: the builtin
-// inside a lambda of a kernel makes the host pass drop the kernel's launch stub.)
-MOE_DEV void buf_ld128_lds(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, off, 0, 0, 0);
-}
 
 // Streaming path: blocks of at most kStreamMaxTiles row subtiles; ring depth (k-steps in
 // flight per wave) for one and for two subtiles (with the group sums of the fold, a 3-deep ring

@@ -37,16 +37,32 @@ MOE_DEV bf16x8_r as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_r, v); }
 
 constexpr int kTileT = 32, kTileE = 64;  // tokens x experts per workgroup
 constexpr int kKSplit = 4;                // waves per workgroup, each a quarter of K
-constexpr int kMfmaRing = 4;              // k-steps of 32 in flight per wave
+constexpr int kStepK = 64;                // k per step: one 128-byte line of every row
+constexpr int kStageRows = kTileT + kTileE;             // rows of one stage: tokens, then experts
+constexpr int kStageLoads = kStageRows / 8;             // 1 KB loads per stage (8 rows each)
+
+// Position of 16-byte chunk c (0..7) of stage row R in LDS (elements). The chunks of a row are
+// XOR-swizzled so that the fragment reads of 16 rows at one chunk fall in distinct bank groups.
+MOE_DEV int stage_chunk(int R, int c) {
+  return R * kStepK + 8 * (c ^ ((R & 7) ^ ((R >> 3) & 1)));
+}
 
 // One workgroup: a 32 x 64 (token x expert) tile of approximate logits as 2 x 4 MFMA 16x16x32
 // tiles; its four waves take a quarter of K each and their partial sums are added through LDS.
-// Lane l loads 8 consecutive bf16 of row (l & 15) of each operand at k = 32 s + 8 (l >> 4):
-// both operands in the same k order, so no permutation is needed. Workgroups of the first
-// token tile also accumulate |w_e|^2 of their expert rows.
+// Operands are staged through LDS, one 64-k step per stage and wave (96 rows x 128 bytes, two
+// stages per wave): each load instruction moves 8 whole 128-byte rows straight into LDS
+// (buffer_load ... lds), so every L1 -> L2 request is a full line. (Loading the MFMA fragments
+// directly, 16 rows x 64 bytes per instruction, made every request a half line, and the kernel
+// was bound by the requests a CU keeps in flight.) Lane (r, kq) then reads row r at chunk
+// 4 S + kq of k-slice S: both operands in the same k order. Workgroups of the first token tile
+// also accumulate |w_e|^2 of their expert rows.
 __global__ __launch_bounds__(64 * kKSplit) void router_mfma_kernel(
     const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ W, int E,
     const float* __restrict__ bias, float* __restrict__ approx, float* __restrict__ nw2) {
+  // Two stages as separate objects: the compiler then knows that reads of one do not wait for
+  // the loads in flight into the other.
+  __shared__ __attribute__((aligned(16))) uint16_t stage0[kKSplit][kStageRows * kStepK];
+  __shared__ __attribute__((aligned(16))) uint16_t stage1[kKSplit][kStageRows * kStepK];
   __shared__ float part[kKSplit][2 * 4][4][64];  // [wave][tile][element][lane]
   __shared__ float s_n2[kKSplit][4][64];
   const int lane = threadIdx.x & 63;
@@ -63,19 +79,32 @@ __global__ __launch_bounds__(64 * kKSplit) void router_mfma_kernel(
   const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, (uint32_t)T * (uint32_t)H * 2u);
   const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W, (uint32_t)E * (uint32_t)H * 2u);
   const int r = lane & 15, kq = lane >> 4;
-  const int steps = H / 32 / kKSplit;  // H % 512 == 0: a multiple of kMfmaRing
-  const uint32_t k0 = (uint32_t)(wv * steps * 32);
-  uint32_t xo[2], wo[4];
+  const int steps = H / kStepK / kKSplit;  // H % 512 == 0: even
+  const uint32_t k0 = (uint32_t)(wv * steps * kStepK);
+
+  // Load q of a stage: lane l fetches row R = 8 q + (l >> 3) at chunk (l & 7) ^ swizzle(R) and
+  // writes it at stage_chunk(R, chunk). Rows 0..31 are tokens t0.., rows 32..95 experts e0..;
+  // a row past T or E gets an out-of-range offset (zeros, no memory access).
+  uint32_t off[kStageLoads];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int t = t0 + 16 * i + r;
-    xo[i] = t < T ? ((uint32_t)t * (uint32_t)H + k0 + 8u * kq) * 2u : kOutOfRange;
+  for (int q = 0; q < kStageLoads; ++q) {
+    const int R = 8 * q + (lane >> 3);
+    const uint32_t c = (uint32_t)((lane & 7) ^ ((R & 7) ^ ((R >> 3) & 1)));
+    if (R < kTileT) {
+      const int t = t0 + R;
+      off[q] = t < T ? ((uint32_t)t * (uint32_t)H + k0 + 8u * c) * 2u : kOutOfRange;
+    } else {
+      const int e = e0 + R - kTileT;
+      off[q] = e < E ? ((uint32_t)e * (uint32_t)H + k0 + 8u * c) * 2u : kOutOfRange;
+    }
   }
+  auto dma = [&](uint16_t* st, int s) {  // a step past the slice loads nothing (zeros, unused)
+    const uint32_t so = s < steps ? (uint32_t)(s * kStepK * 2) : kOutOfRange;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = e0 + 16 * j + r;
-    wo[j] = e < E ? ((uint32_t)e * (uint32_t)H + k0 + 8u * kq) * 2u : kOutOfRange;
-  }
+    for (int q = 0; q < kStageLoads; ++q)
+      buf_ld128_lds(q < kTileT / 8 ? xr : wr, st + q * 8 * kStepK, off[q] + so);
+  };
+
   const bool norms = tt == 0;  // workgroup-uniform
   float n2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   f32x4 acc[2][4];
@@ -84,50 +113,62 @@ __global__ __launch_bounds__(64 * kKSplit) void router_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 a[kMfmaRing][2], b[kMfmaRing][4];
-  auto load = [&](int s, int slot) {
-    const uint32_t so = s < steps ? (uint32_t)s * 64u : kOutOfRange;
+  auto compute = [&](const uint16_t* st) {
+    u32x4 a[2][2], b[4][2];  // [subtile][k-slice]
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      a[slot][i] = buf_ld128(xr, (xo[i] + so) | (so & kOutOfRange) | (xo[i] & kOutOfRange));
+    for (int S = 0; S < 2; ++S) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      b[slot][j] = buf_ld128(wr, (wo[j] + so) | (so & kOutOfRange) | (wo[j] & kOutOfRange));
-  };
-  auto compute = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
+        a[i][S] = *reinterpret_cast<const u32x4*>(st + stage_chunk(16 * i + r, 4 * S + kq));
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[slot][i]),
-                                                            as_bf16x8(b[slot][j]), acc[i][j], 0,
-                                                            0, 0);
+        b[j][S] = *reinterpret_cast<const u32x4*>(st + stage_chunk(kTileT + 16 * j + r,
+                                                                     4 * S + kq));
+    }
+#pragma unroll
+    for (int S = 0; S < 2; ++S)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i][S]),
+                                                              as_bf16x8(b[j][S]), acc[i][j], 0,
+                                                              0, 0);
     if (norms) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float lo = bf16lo_to_f32(b[slot][j][d]), hi = bf16hi_to_f32(b[slot][j][d]);
-          n2[j] = __builtin_fmaf(lo, lo, n2[j]);
-          n2[j] = __builtin_fmaf(hi, hi, n2[j]);
-        }
+        for (int S = 0; S < 2; ++S)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const float lo = bf16lo_to_f32(b[j][S][d]), hi = bf16hi_to_f32(b[j][S][d]);
+            n2[j] = __builtin_fmaf(lo, lo, n2[j]);
+            n2[j] = __builtin_fmaf(hi, hi, n2[j]);
+          }
     }
   };
-  // The ring's first stages issued in step order, so that the wait before each step of the loop
-  // is for that step's stage only, on the first entry as on the back-edge (scheduled freely,
-  // slot 0's loads went out last and the wait at the loop head drained all but the newest stage).
-#pragma unroll
-  for (int j = 0; j < kMfmaRing - 1; ++j) {
-    load(j, j);
+
+  // Two stages per wave (the wave's own LDS, no barrier): the wait at the top of a step is for
+  // that step's loads only; the next step's stay in flight. A stage is refilled once its
+  // fragments are in registers.
+  uint16_t* const s0 = stage0[wv];
+  uint16_t* const s1 = stage1[wv];
+  dma(s0, 0);
+  __builtin_amdgcn_sched_barrier(0);  // issue order = step order
+  dma(s1, 1);
+  for (int s = 0; s < steps; s += 2) {
     __builtin_amdgcn_sched_barrier(0);
-  }
-  for (int s0 = 0; s0 < steps; s0 += kMfmaRing) {
-#pragma unroll
-    for (int j = 0; j < kMfmaRing; ++j) {
-      load(s0 + j + kMfmaRing - 1, (j + kMfmaRing - 1) % kMfmaRing);
-      __builtin_amdgcn_sched_barrier(0);  // the ring's next loads ahead of this step's wait
-      compute(j);
-    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kStageLoads));
+    compute(s0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage 0's reads done before it is refilled
+    __builtin_amdgcn_sched_barrier(0);
+    dma(s0, s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kStageLoads));
+    compute(s1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_sched_barrier(0);
+    dma(s1, s + 3);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
