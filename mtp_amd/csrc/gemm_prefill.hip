@@ -136,20 +136,26 @@ MOE_DEV void static_for(F&& f) {
 // ---- Streaming path for blocks whose slots fit in MT row subtiles (an expert with few tokens).
 // Such a block reads its 128 KB-per-wave weight slice for very little arithmetic, so its time is
 // memory latency: with the LDS-staged path's one-step lookahead every 128-k step waits for a
-// full round trip. Here each wave keeps D k-steps in flight in registers - the A fragments of
-// its MT row subtiles, the packed weight words and the step's scales and zeros, all buffer loads
-// (steps past K read zeros without a memory access) - and uses no LDS and no barrier. The
-// dequant is the folded one (compute_fold).
+// full round trip. Here each wave keeps D k-steps of its packed weight words and scales and zeros
+// in flight in registers. The block's A rows (MT*16 x 128 k per step) go through a D-stage LDS
+// ring filled by buffer_load ... lds, each wave loading MT of the stage's 1 KB runs: whole
+// 128-byte lines, once per workgroup (fragments loaded by every wave straight from memory were 16
+// half-line requests per instruction, repeated by the four waves). Steps past K read zeros
+// without a memory access. The dequant is the folded one (compute_fold).
 template <int MT>
 struct StreamStage {
-  u32x4 a[MT][4];  // row mi*16 + j, 8 consecutive bf16 at k = 32 kk + 8 kq
   u32x4 bw[4];     // packed words of the lane's 4 columns, k-slice kk
   GroupSZ gz[2];   // groups of k-slices 0-1 and 2-3
 };
 
 struct StreamView {
   __amdgpu_buffer_rsrc_t ar;  // A rows (uniform)
-  uint32_t a_off[2];          // lane row offsets (+ 8 kq bf16), kOutOfRange for a padding row
+  // A ring: stage i of MT*16 rows x BK in LDS object lds[i] (separate objects, so that the
+  // compiler's waits for the loads into one stage do not cover reads of another); rows swizzled
+  // as in the LDS path.
+  uint16_t* lds[4];
+  uint32_t a_dma[2];          // this wave's DMA lane offsets at step 0, kOutOfRange for padding rows
+  int wave, j, kq;
   // The lane's weights: in W1 lanes j < 8 read gate and lanes j >= 8 up, so these are per-lane
   // global addresses rather than buffer resources.
   const int32_t* bq;          // packed row kq of step 0 at the lane's first column
@@ -157,8 +163,18 @@ struct StreamView {
   const int32_t* bz;          // zeros word of group 0 holding the lane's columns
   int NOUT, gsh, nsteps, zsh;  // gsh: log2 of the group size
 
-  // Step s of the ring; a prefetch past the last step re-reads the last step (in bounds; it is
-  // never multiplied), so every pass issues the same loads.
+  // A rows of step s into LDS stage `slot`: load u of this wave is run q = wave * MT + u (rows
+  // 4q .. 4q + 3). A step past K writes zeros (never read).
+  template <int MT>
+  MOE_DEV void dma(int s, int slot) const {
+    const uint32_t ks = (uint32_t)s * BK * 2u, oob = s < nsteps ? 0u : kOutOfRange;
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+      buf_ld128_lds(ar, lds[slot] + 4 * (wave * MT + u) * BK, (a_dma[u] + ks) | oob);
+  }
+
+  // Weights, scales and zeros of step s; a prefetch past the last step re-reads the last step
+  // (in bounds; it is never multiplied), so every pass issues the same loads.
   template <int MT>
   MOE_DEV void load(StreamStage<MT>& st, int s) const {
     const int sc = min(s, nsteps - 1);
@@ -171,26 +187,24 @@ struct StreamView {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)  // weights are streamed once: nontemporal
       st.bw[kk] = ld128_nt(bq + (int64_t)(sc * (BK / 8) + kk * 4) * NOUT);
-    const uint32_t ka = (uint32_t)sc * BK * 2u;
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) st.a[mi][kk] = buf_ld128(ar, a_off[mi] + ka + 64u * kk);
   }
 
   // Folded form of compute for step `step`: group sums in gs / gx, folded into acc at the end of
   // each quantisation group (group sizes >= 64, so a group ends at a half-step boundary).
   template <int MT>
-  MOE_DEV void compute_fold(const StreamStage<MT>& st, int step, f32x4 (&acc)[MT][4],
+  MOE_DEV void compute_fold(const StreamStage<MT>& st, int step, int slot, f32x4 (&acc)[MT][4],
                             f32x4 (&gs)[MT][4], f32x4 (&gx)[MT]) const {
     const bf16x8_v ones =
         __builtin_bit_cast(bf16x8_v, u32x4{kFoldOnes, kFoldOnes, kFoldOnes, kFoldOnes});
+    // A fragment of row mi*16 + j at chunk 4 kk + kq (stored at chunk position (4 kk + kq) ^ j)
+    const uint16_t* la = lds[slot] + j * BK;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       bf16x8_v af[MT];
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi) {
-        af[mi] = fold_act_frag(st.a[mi][kk]);
+        af[mi] = fold_act_frag(
+            *reinterpret_cast<const u32x4*>(la + mi * 16 * BK + 8 * ((4 * kk + kq) ^ j)));
         gx[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], ones, gx[mi], 0, 0, 0);
       }
 #pragma unroll
@@ -226,13 +240,18 @@ struct StreamView {
   }
 };
 
-// acc += A[MT*16 rows, :K] . B[:K, lane columns] over all steps with a D-deep register ring.
-// NS > 0: exactly NS steps as straight-line code, so each wait is for exactly the step about to be
-// multiplied. NS == 0: a runtime loop (D divides the step count) whose body issues the same loads
-// on every pass; its waits are exact only for D == 2 (a deeper ring makes the loop head wait for
-// all but the newest stage).
+// acc += A[MT*16 rows, :K] . B[:K, lane columns] over all steps with a D-deep ring (registers for
+// B, LDS for A). Step st: the B loads of step st + D - 1; the wait for this wave's loads of step
+// st (A and B; the later steps' stay in flight); a barrier (every wave's A of step st landed, and
+// every wave is done with the stage that step st + D - 1 refills); the A loads of step st + D - 1;
+// the multiplications of step st. NS > 0: exactly NS steps as straight-line code. NS == 0: a
+// runtime loop (D divides the step count) whose body issues the same loads on every pass.
 template <int MT, int D, int NS>
 MOE_DEV void stream_block(const StreamView& v, f32x4 (&acc)[MT][4]) {
+  static_assert(D <= 4 && (D <= 2 || MT == 1), "A stages 2 and 3 hold 16 rows");
+  // loads issued after step st's A loads when step st is waited for: B of steps st+1 .. st+D-1
+  // and A of steps st+1 .. st+D-2
+  constexpr int kLater = 8 * (D - 1) + MT * (D - 2);
   StreamStage<MT> ring[D];
   f32x4 gs[MT][4], gx[MT];
 #pragma unroll
@@ -243,22 +262,39 @@ MOE_DEV void stream_block(const StreamView& v, f32x4 (&acc)[MT][4]) {
   }
   static_for<0, D - 1>([&](auto jc) {
     v.load(ring[jc.value], jc.value);
+    v.template dma<MT>(jc.value, jc.value);
     __builtin_amdgcn_sched_barrier(0);  // issue order = step order
   });
+  // LATER: loads issued after step st's A loads when step st is waited for (kLater while the
+  // ring is refilled; in the straight-line tail, the (8 + MT) loads of each step still to come)
+  auto step = [&](auto slot_c, auto later_c, int st, bool more) {
+    constexpr int slot = decltype(slot_c)::value;
+    constexpr int refill = (slot + D - 1) % D;  // the stage of step st + D - 1
+    if (more) v.load(ring[refill], st + D - 1);
+    __builtin_amdgcn_sched_barrier(0);  // this step's B loads ahead of the wait for step st
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(decltype(later_c)::value));
+    // The barrier without __syncthreads' release fence, which would also wait for the A loads
+    // of the later stages still in flight. Each wave has waited for its own loads of step st,
+    // which are then in LDS for every wave; the signal fences keep the compiler from moving
+    // LDS accesses across the barrier.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (more) v.template dma<MT>(st + D - 1, refill);
+    __builtin_amdgcn_sched_barrier(0);
+    v.compute_fold(ring[slot], st, slot, acc, gs, gx);
+  };
   if constexpr (NS > 0) {
     static_for<0, NS>([&](auto sc) {
       constexpr int st = sc.value;
-      if constexpr (st + D - 1 < NS) v.load(ring[(st + D - 1) % D], st + D - 1);
-      __builtin_amdgcn_sched_barrier(0);  // this stage's loads ahead of the wait for step st
-      v.compute_fold(ring[st % D], st, acc, gs, gx);
+      constexpr bool more = st + D - 1 < NS;
+      step(std::integral_constant<int, st % D>{},
+           std::integral_constant<int, more ? kLater : (NS - 1 - st) * (8 + MT)>{}, st, more);
     });
   } else {
     for (int s0 = 0; s0 < v.nsteps; s0 += D) {
       static_for<0, D>([&](auto jc) {
-        constexpr int jj = jc.value;
-        v.load(ring[(jj + D - 1) % D], s0 + jj + D - 1);
-        __builtin_amdgcn_sched_barrier(0);
-        v.compute_fold(ring[jj], s0 + jj, acc, gs, gx);
+        step(jc, std::integral_constant<int, kLater>{}, s0 + jc.value, true);
       });
     }
   }
@@ -333,6 +369,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   // for the LDS loads in flight into the other.
   __shared__ __attribute__((aligned(16))) uint16_t lds_a0[BM * BK];
   __shared__ __attribute__((aligned(16))) uint16_t lds_a1[BM * BK];
+  // Two more stages of the streaming path's A ring (16 rows each; stages 0 and 1 are lds_a0, lds_a1)
+  __shared__ __attribute__((aligned(16))) uint16_t lds_s2[16 * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_s3[16 * BK];
   __shared__ int s_slot[BM];
   __shared__ float s_w[MODE == MODE_W2 ? BM : 1];  // routed weight of each row (W2)
 
@@ -409,13 +448,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, a_bytes, kBufferDword3);
     StreamView v;
     v.ar = ar;
+    v.lds[0] = lds_a0;
+    v.lds[1] = lds_a1;
+    v.lds[2] = lds_s2;  // 16 rows: stages 2 and 3 serve one-subtile blocks only
+    v.lds[3] = lds_s3;
+    v.wave = wave;
+    v.j = j;
+    v.kq = kq;
+    // DMA run q = wave * MT + u: lane i fetches row 4q + (i >> 4) at chunk (i & 15) ^ (row & 15)
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-      const int f = s_slot[mi * 16 + j];
+    for (int u = 0; u < 2; ++u) {
+      const int r = 4 * (wave * mt_u + u) + (lane >> 4);
+      const int f = s_slot[r];
       const uint32_t arow = (MODE == MODE_W1) ? slot_token(sd, f) : f;
-      v.a_off[mi] = ((unsigned)f < (unsigned)sd.num_slots)
-                        ? (arow * (uint32_t)K + 8u * kq) * 2u
-                        : kOutOfRange;
+      const uint32_t c = (uint32_t)((lane & 15) ^ (r & 15));
+      v.a_dma[u] = ((unsigned)f < (unsigned)sd.num_slots) ? (arow * (uint32_t)K + 8u * c) * 2u
+                                                           : kOutOfRange;
     }
     v.bq = bq;
     v.bs = bs;
