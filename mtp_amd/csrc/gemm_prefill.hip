@@ -23,8 +23,9 @@
 //       (lanes j >= 8); the epilogue pairs them with a row rotation by 8 and writes bf16 h.
 //   W2: 64 output columns of the hidden dimension; epilogue writes w[slot] * acc (fp32 or bf16).
 // 16-row subtiles that hold only padding are neither loaded nor multiplied. Blocks with at most
-// two subtiles of slots (experts with few tokens) take a streaming path instead: no LDS, a
-// register ring several k-steps deep, folded dequant (see stream_block). There the exact
+// two subtiles of slots (experts with few tokens) take a streaming path instead: B in a register
+// ring several k-steps deep, A in a ring of LDS stages of the same depth, folded dequant (see
+// stream_block). There the exact
 // dequant's ~19 VALU operations per packed word cost more than the multiplications they feed;
 // the fold needs 7 per word plus two per output element and group (measured: prefill-2048
 // 259 -> 248 us per layer).
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void grouped_gemm_kernel(
   const int32_t* bz = pr.qzeros + (col >> 3);
   const int zsh = 4 * (col & 7);
 
-  // Few slots: the streaming path (no LDS, a register ring several k-steps deep).
+  // Few slots: the streaming path (B in a register ring several k-steps deep, A in LDS stages).
   const int mt_u = __builtin_amdgcn_readfirstlane(mtiles);
   if (mt_u <= kStreamMaxTiles) {
     const __amdgpu_buffer_rsrc_t ar =
