@@ -11,7 +11,13 @@
  *   - every tensor pointer is a DEVICE pointer owned by the caller;
  *   - `stream` is a hipStream_t (NULL = the null stream); calls are stream-ordered,
  *     never synchronise the host and never allocate device memory;
- *   - bf16 and fp16 values travel as uint16_t bit patterns.
+ *   - bf16 and fp16 values travel as uint16_t bit patterns;
+ *   - versioning: the _v1 suffix names the interface family, not its layout. Signatures and
+ *     structs may change between releases under the same name (moe_sum_v1 gained topk_ids,
+ *     num_experts and expert_row in ABI version 2, and moe_slot_cache_counters_v1 its two
+ *     ready-time fields); MOE_W4A16_ABI_VERSION is bumped whenever any of them does. A caller
+ *     must check moe_w4a16_abi_version() == MOE_W4A16_ABI_VERSION of the header it was built
+ *     against before any other call (the Python binding refuses to load on a mismatch).
  *
  * Tensor layouts are the reference's repacked GPTQ layout
  * (src/mtp_expert_prefetch/repack/qwen3_moe_gptq.py:142-198, store.py:126-137),
@@ -70,7 +76,8 @@ typedef struct moe_expert_set_v1 {
 /* Kernel path selection for the expert GEMMs (block_m: 16 for DECODE, 128 for PREFILL).
  *   DECODE : MFMA 16x16x32 bf16 on 16-slot blocks, int4 dequantised in registers into the
  *            MFMA operand, K split across waves (token batches up to a few hundred slots);
- *   PREFILL: MFMA on 128-slot blocks with dequantised int4 tiles staged in LDS;
+ *   PREFILL: MFMA on 128-slot blocks, activation tiles staged in LDS, int4 dequantised in
+ *            registers into the MFMA operand;
  *   AUTO   : PREFILL when T * top_k >= 1024, else DECODE.
  * Any other value is refused with MOE_ERR_UNSUPPORTED (the workspace query returns -1). */
 enum { MOE_PATH_AUTO = 0, MOE_PATH_DECODE = 1, MOE_PATH_PREFILL = 2 };

@@ -434,7 +434,15 @@ int moe_rmsnorm_v1(uint16_t* res, const uint16_t* add, int32_t T, int32_t hidden
   if (!(eps >= 0.0f)) return fail(MOE_ERR_SHAPE, "rmsnorm: eps must be >= 0");
   if (T == 0) return MOE_OK;
   if (!res || !weight || !out) return fail(MOE_ERR_NULL, "rmsnorm: NULL pointer");
-  if (out == res) return fail(MOE_ERR_SHAPE, "rmsnorm: out must not alias res");
+  {  // the [T, hidden] bf16 row sets res (updated in place), add and out share no byte
+    const uintptr_t rows = (uintptr_t)T * hidden * 2;
+    auto overlap = [rows](const void* a, const void* b) {
+      const uintptr_t p = (uintptr_t)a, q = (uintptr_t)b;
+      return a && b && p < q + rows && q < p + rows;
+    };
+    if (overlap(out, res) || overlap(out, add) || overlap(add, res))
+      return fail(MOE_ERR_SHAPE, "rmsnorm: out, res and add must not overlap");
+  }
   MOE_CHECK_HIP(launch_rmsnorm(res, add, T, hidden, weight, eps, res, out, (hipStream_t)stream),
                 "rmsnorm");
   return MOE_OK;
@@ -449,6 +457,26 @@ int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_
 }
 
 }  // extern "C"
+
+// The argument checks of a routed layer call before any workspace is involved, shared by
+// moe_layer_v1, moe_norm_layer_v1 and moe_layer_noalloc_v1 so that one bad input gets one error
+// code from all of them. T == 0 passes (the call is then a no-op).
+int check_layer_args(const uint16_t* x, int32_t T, const uint16_t* router_w, int32_t top_k,
+                     const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                     const uint16_t* shared_gate_w, const uint16_t* out, int32_t path) {
+  int rc = check_experts(experts, shared);
+  if (rc) return rc;
+  if (T < 0) return fail(MOE_ERR_SHAPE, "layer: T=%d", T);
+  if (T == 0) return MOE_OK;
+  if (!x || !router_w || !out) return fail(MOE_ERR_NULL, "layer: NULL pointer");
+  if (shared && !shared_gate_w) return fail(MOE_ERR_NULL, "layer: shared expert needs shared_gate_w");
+  const int E = experts->num_experts;
+  if (top_k < 1 || top_k > E || top_k > 64)
+    return fail(MOE_ERR_SHAPE, "layer: top_k=%d outside [1, min(num_experts, 64)]", top_k);
+  if (resolve_path(path, T, top_k) < 0)
+    return fail(MOE_ERR_UNSUPPORTED, "layer: unknown path %d", path);
+  return MOE_OK;
+}
 
 namespace {
 
@@ -467,19 +495,13 @@ int layer_impl(const uint16_t* x, int32_t T, const uint16_t* router_w, const flo
                const uint16_t* shared_gate_w, void* workspace, int64_t workspace_bytes,
                uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out, int32_t path,
                void* stream, const PreNorm* pn) {
-  int rc = check_experts(experts, shared);
-  if (rc) return rc;
-  if (T < 0) return fail(MOE_ERR_SHAPE, "layer: T=%d", T);
-  if (T == 0) return MOE_OK;
   if (pn) x = pn->x_out;
-  if (!x || !router_w || !out || !workspace) return fail(MOE_ERR_NULL, "layer: NULL pointer");
-  if (shared && !shared_gate_w) return fail(MOE_ERR_NULL, "layer: shared expert needs shared_gate_w");
+  int rc = check_layer_args(x, T, router_w, top_k, experts, shared, shared_gate_w, out, path);
+  if (rc) return rc;
+  if (T == 0) return MOE_OK;
+  if (!workspace) return fail(MOE_ERR_NULL, "layer: NULL pointer");
   const int E = experts->num_experts;
-  if (top_k < 1 || top_k > E || top_k > 64)
-    return fail(MOE_ERR_SHAPE, "layer: top_k=%d outside [1, min(num_experts, 64)]", top_k);
-  const int path_in = path;
   path = resolve_path(path, T, top_k);
-  if (path < 0) return fail(MOE_ERR_UNSUPPORTED, "layer: unknown path %d", path_in);
   const Workspace L = layout(T, top_k, experts, shared ? 1 : 0, path);
   if (workspace_bytes < (int64_t)L.total)
     return fail(MOE_ERR_WORKSPACE, "layer: workspace %lld < required %lld",
@@ -567,10 +589,21 @@ int moe_norm_layer_v1(const uint16_t* res_in, const uint16_t* add, const uint16_
   if (H <= 0 || H % 8 != 0 || H > 8192)
     return fail(MOE_ERR_SHAPE, "norm layer: hidden=%d (hidden %% 8 == 0, <= 8192)", H);
   if (!(eps >= 0.0f)) return fail(MOE_ERR_SHAPE, "norm layer: eps must be >= 0");
-  if (x_out == res_in || x_out == res_out || (add && (x_out == add || res_out == add)))
-    return fail(MOE_ERR_SHAPE, "norm layer: x_out and add must not alias the residual rows");
-  if (out == x_out || out == res_in || out == res_out)
-    return fail(MOE_ERR_SHAPE, "norm layer: out must not alias x_out or the residual rows");
+  // Byte ranges of the [T, H] bf16 row sets: the residual may be updated in place (res_out ==
+  // res_in: every row is read and written by one workgroup), but no other pair may share bytes
+  // (a row-offset overlap would let one workgroup overwrite rows another still reads).
+  const size_t rows = (size_t)T * H * 2;
+  auto overlap = [rows](const void* a, const void* b) {
+    const uintptr_t p = (uintptr_t)a, q = (uintptr_t)b;
+    return a && b && p < q + rows && q < p + rows;
+  };
+  if (res_out != res_in && overlap(res_out, res_in))
+    return fail(MOE_ERR_SHAPE, "norm layer: res_out must equal res_in or not overlap it");
+  if (overlap(x_out, res_in) || overlap(x_out, res_out) || overlap(x_out, add) ||
+      overlap(res_out, add) || overlap(res_in, add))
+    return fail(MOE_ERR_SHAPE, "norm layer: x_out and add must not overlap the residual rows");
+  if (overlap(out, x_out) || overlap(out, res_in) || overlap(out, res_out))
+    return fail(MOE_ERR_SHAPE, "norm layer: out must not overlap x_out or the residual rows");
   const PreNorm pn{res_in, add, norm_w, eps, res_out, x_out};
   return layer_impl(nullptr, T, router_w, logit_bias, top_k, experts, shared, shared_gate_w,
                     workspace, workspace_bytes, out, topk_ids_out, topk_weights_out, path, stream,

@@ -10,6 +10,12 @@
 constexpr int kErrorBufferBytes = 512;
 char* moe_error_buffer();
 
+// Argument checks of a routed layer call that involve no workspace (api.hip): 0 or the error
+// code moe_layer_v1 returns for the same input (message in moe_error_buffer).
+int check_layer_args(const uint16_t* x, int32_t T, const uint16_t* router_w, int32_t top_k,
+                     const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
+                     const uint16_t* shared_gate_w, const uint16_t* out, int32_t path);
+
 struct ProjDev;
 struct ExpertsDev;
 struct SlotsDev;

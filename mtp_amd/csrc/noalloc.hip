@@ -67,10 +67,10 @@ int moe_layer_noalloc_v1(const uint16_t* x, int32_t T, const uint16_t* router_w,
                          const moe_expert_set_v1* shared, const uint16_t* shared_gate_w,
                          uint16_t* out, int32_t* topk_ids_out, float* topk_weights_out,
                          int32_t path, void* stream) {
-  if (!experts) {
-    snprintf(moe_error_buffer(), kErrorBufferBytes, "experts is NULL");
-    return MOE_ERR_NULL;
-  }
+  // moe_layer_v1's own argument checks first: the same bad input gets the same error code
+  const int rc0 = check_layer_args(x, T, router_w, top_k, experts, shared, shared_gate_w, out,
+                                   path);
+  if (rc0 || T == 0) return rc0;
   const int64_t need = moe_layer_workspace_bytes_v1(T, top_k, experts, shared ? 1 : 0, path);
   if (need < 0) {
     snprintf(moe_error_buffer(), kErrorBufferBytes, "noalloc: invalid sizes T=%d top_k=%d", T,

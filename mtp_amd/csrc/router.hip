@@ -299,8 +299,12 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
   return launch_logits_tiled<8, 8>(x, T, H, W, E, shared_w, bias, logits, stream);
 }
 
+// The fused form writes the new residual from one workgroup per token tile while the others
+// still read res_in: the two row sets must not share any byte (in place included).
 bool router_norm_fits(int T, int H, const void* res_in, const void* res_out) {
-  return T >= 1 && T <= 64 && H >= 8 && H <= kNormChunk && H % 8 == 0 && res_in != res_out;
+  const uintptr_t p = (uintptr_t)res_in, q = (uintptr_t)res_out, rows = (uintptr_t)T * H * 2;
+  return T >= 1 && T <= 64 && H >= 8 && H <= kNormChunk && H % 8 == 0 &&
+         (p + rows <= q || q + rows <= p);
 }
 
 hipError_t launch_router_logits_norm(const uint16_t* res_in, const uint16_t* add,

@@ -18,7 +18,10 @@
 //    pins). A prefetch that finds only pinned slots skips that expert;
 //  * a prefetch first makes both copy streams wait for all work enqueued so far on the compute
 //    stream, so an unpinned slot is never overwritten while an enqueued kernel may read it;
-//    its copies alternate between the two streams.
+//  * every prefetch copy into slot s goes to copy stream s % kCopyStreams, so two copies into
+//    one slot (a list longer than the unpinned slots, or two prefetch calls with no demand
+//    between them) run in issue order and the slot ends with the bytes of the expert its table
+//    entry names.
 // The table entry of an absent expert is -1: the kernels drop the slots routed to it (they
 // contribute zero). Handles are not thread-safe: one handle per host thread.
 //
@@ -46,8 +49,8 @@ constexpr uint64_t kMagic = 0x4D4F45534C4F5431ull;  // "MOESLOT1"
 constexpr int kStagingRing = 512;
 constexpr int kEventRing = 1024;  // timing events of prefetch calls and of demands
 // Copy streams of the prefetches: one DMA stream moves about 42 GB/s of expert blobs from
-// pinned host memory, two together about 53 GB/s, four no more (MI355X, measured); copies
-// alternate. (Splitting a demand's misses over the compute stream and a second stream measured
+// pinned host memory, two together about 53 GB/s, four no more (MI355X, measured); a slot's
+// copies always use the same stream (slot index modulo the count). (Splitting a demand's misses over the compute stream and a second stream measured
 // slower: the cross-stream wait costs more than the parallel copy saves.)
 constexpr int kCopyStreams = 2;
 
@@ -84,7 +87,6 @@ struct Cache {
   uint64_t tick = 0;
   hipStream_t side[kCopyStreams] = {};  // prefetch copies
   hipEvent_t compute_mark = nullptr;
-  int copy_rr = 0;                      // copy stream of the next prefetch copy
   int32_t* staging = nullptr;  // pinned [kStagingRing][num_experts]
   std::vector<hipEvent_t> staging_done;
   int staging_next = 0;
@@ -281,8 +283,7 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
     }
     c->st.issued_fetch_count++;
     evict(c, L, s);
-    const int cs_i = c->copy_rr;
-    c->copy_rr = (c->copy_rr + 1) % kCopyStreams;
+    const int cs_i = s % kCopyStreams;  // one stream per slot: its copies stay in order
     L.slots[s] = Slot{e, true, false, false, ++c->tick, live(c) ? c->pf_seq + 1 : 0, cs_i};
     L.slot_of[e] = s;
     ++count;
@@ -362,7 +363,11 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
       Slot& sl = L.slots[s];
       if (sl.prefetched && !sl.used) {
         c->st.used_fetch_count++;
-        if (dseq && sl.pf_seq) c->checks.push_back(ReadyCheck{sl.pf_seq, sl.pf_stream, dseq});
+        // The copy's timing event is only still its own while fewer than kEventRing prefetch
+        // calls have recorded since; an older copy completed long before this demand (counted
+        // on time).
+        if (dseq && sl.pf_seq && c->pf_seq - sl.pf_seq < (uint64_t)kEventRing)
+          c->checks.push_back(ReadyCheck{sl.pf_seq, sl.pf_stream, dseq});
       }
       sl.used = true;
       sl.pinned = true;

@@ -112,3 +112,21 @@ def test_moe_sum_requires_the_routed_ids():
     lib = _lib.load()
     rc = lib.moe_sum_v1(0x10, 4, 8, 2048, 0, None, 256, None, 0x10, None)
     assert rc == _lib.MOE_ERR_NULL
+
+
+@pytest.mark.parametrize("T,top_k,path,E", [(16, 8, 3, 256), (16, 8, -1, 256), (16, 65, 0, 256),
+                                            (4, 20, 1, 16), (4, 0, 0, 256), (-1, 8, 0, 256)])
+def test_noalloc_entry_reports_the_workspace_entrys_error_codes(T, top_k, path, E):
+    """moe_layer_noalloc_v1 runs moe_layer_v1's argument checks before its scratch-size check:
+    an unknown path, a top_k outside [1, min(E, 64)] or a negative T get the same code and
+    message from both entry points (checked on the host; nothing is launched)."""
+    lib = _lib.load()
+    ex = _fake_set(E=E)
+    rc_ws = lib.moe_layer_v1(0x10, T, 0x10, None, top_k, ctypes.byref(ex), None, None, 0x10,
+                             1 << 40, 0x10, None, None, path, None)
+    msg_ws = lib.moe_w4a16_last_error()
+    rc_na = lib.moe_layer_noalloc_v1(0x10, T, 0x10, None, top_k, ctypes.byref(ex), None, None,
+                                     0x10, None, None, path, None)
+    assert rc_ws != _lib.MOE_OK
+    assert rc_na == rc_ws
+    assert lib.moe_w4a16_last_error() == msg_ws

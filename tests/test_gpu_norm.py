@@ -162,3 +162,32 @@ def test_norm_layer_chain_equals_unfused_chain():
     torch.cuda.synchronize()
     assert torch.equal(y_b, y_a)
     assert torch.equal(bufs[cur], res_a)
+
+
+def test_norm_layer_rejects_partly_overlapping_rows():
+    """A residual output that overlaps the input rows at a row offset (not the same rows, which
+    is the in-place update) is refused before any launch, as are overlaps of x_out or out with the
+    residual rows; the separate rmsnorm refuses overlaps of out, res and add."""
+    from mtp_amd._lib import MoeLibraryError
+    _say("norm layer partial overlap")
+    layer = to_gpu(synth.make_layer(9, num_experts=32, hidden=512, intermediate=512))
+    T, H = 4, 512
+    buf = torch.randn(2 * T, H).to(torch.bfloat16).cuda()
+    nw = torch.zeros(H, dtype=torch.bfloat16, device="cuda")
+    res = buf[:T]
+    with pytest.raises(MoeLibraryError, match="res_out must equal res_in or not overlap"):
+        ops.norm_layer(res, layer.router_w, layer.experts, nw, res_out=buf[1:T + 1], top_k=4,
+                       path="decode")
+    with pytest.raises(MoeLibraryError, match="must not overlap"):
+        ops.norm_layer(res, layer.router_w, layer.experts, nw, x_out=buf[T - 1:2 * T - 1],
+                       top_k=4, path="decode")
+    with pytest.raises(MoeLibraryError, match="must not overlap"):
+        ops.rmsnorm(res, nw, out=buf[2:T + 2])
+    torch.cuda.synchronize()
+    # disjoint views of the same buffer are fine, and so is the in-place update
+    y, r, _ = ops.norm_layer(buf[:T], layer.router_w, layer.experts, nw, res_out=buf[T:],
+                             top_k=4, path="decode")
+    y2, r2, _ = ops.norm_layer(buf[T:].clone(), layer.router_w, layer.experts, nw, top_k=4,
+                               path="decode")
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)

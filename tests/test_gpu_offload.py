@@ -197,7 +197,63 @@ def test_prefetch_between_demand_and_kernels_keeps_demanded_slots(pooled):
     want = ops.fused_experts(x, ids, w, g.experts, path="decode")
     torch.cuda.synchronize()
     assert torch.equal(got, want)
-    _slot_bytes_ok(pool, layer, demanded, pack_blobs(g.experts))
+    blobs = pack_blobs(g.experts)
+    _slot_bytes_ok(pool, layer, demanded, blobs)
+    # every prefetched expert that is resident holds its own bytes: the list was longer than the
+    # unpinned slots, so some slots were filled twice within the one call
+    _slot_bytes_ok(pool, layer, [e for e in others if pool.cache.slot_of(layer, e) >= 0], blobs)
+
+
+def test_repeated_prefetches_into_one_slot_keep_the_last_experts_bytes():
+    """Prefetch calls with no demand between them refill the same LRU slots: with one slot per
+    layer every call overwrites it, and the slot must end with the bytes of the expert its table
+    entry names (the copies into one slot run in issue order)."""
+    E, H, I = 16, 512, 256
+    g = to_gpu(small_layer(3))
+    blobs = pack_blobs(g.experts)
+    for slots in (1, 3):
+        pool = OffloadedExperts(1, E, H, I, slots, group_size=128, device="cuda")
+        try:
+            pool.store_layer(0, g.experts)
+            torch.cuda.synchronize()
+            for rep in range(4):
+                _say(f"  slots={slots} rep={rep}")
+                pool.prefetch(0, [(5 * rep + i) % E for i in range(7)])
+                pool.prefetch(0, [(3 * rep + 11 + i) % E for i in range(5)])
+                torch.cuda.synchronize()
+                resident = [e for e in range(E) if pool.cache.slot_of(0, e) >= 0]
+                assert len(resident) == slots
+                _slot_bytes_ok(pool, 0, resident, blobs)
+        finally:
+            pool.close()
+
+
+def test_demand_of_a_prefetch_older_than_the_event_ring_is_on_time():
+    """A prefetched expert first demanded after more prefetch calls than the handle keeps timing
+    events for (1024): its own event has been re-recorded by a later call (here on another layer,
+    still in flight when the demand is issued), so the check is skipped and the expert counts as
+    on time, not as a ready-late miss measured against an unrelated copy."""
+    E, H, I = 16, 512, 256
+    g = to_gpu(small_layer(4))
+    pool = OffloadedExperts(2, E, H, I, 2, group_size=128, device="cuda")
+    try:
+        pool.store_layer(0, g.experts)
+        pool.store_layer(1, g.experts)
+        torch.cuda.synchronize()
+        pool.prefetch(0, [3])
+        torch.cuda.synchronize()
+        _say("  1100 prefetch calls on layer 1")
+        for i in range(1100):  # each call issues one copy (two slots, three experts in turn)
+            assert pool.prefetch(1, [i % 3]) == 1
+        pool.demand(0, [3])
+        pool.layer_done(0)
+        torch.cuda.synchronize()
+        st = pool.stats()
+        assert st["demand_hit_count"] == 1 and st["used_fetch_count"] == 1
+        assert st["ready_late_miss_count"] == 0, st
+        _slot_bytes_ok(pool, 0, [3], pack_blobs(g.experts))
+    finally:
+        pool.close()
 
 
 def test_store_loads_into_hbm_stacks_and_the_pinned_pool(tmp_path):
