@@ -573,7 +573,7 @@ def offload_bench(layers, args, dev) -> dict:
         fresh = pool
         dec = OffloadDecoder(fresh, routers, biases, top_k=K, predictor=predictor, prefetch_k=k,
                              path="decode")
-        step_s, base = [], None
+        step_s, base, trace = [], None, []
         for t in range(n_tok):
             if t == args.offload_warmup:
                 torch.cuda.synchronize()
@@ -583,10 +583,16 @@ def offload_bench(layers, args, dev) -> dict:
                 pre = true_lists[t + 1]
             else:
                 pre = dec.predict(hs[t + 1])
-            dec.step(xs[t], pre)
+            outs = dec.step(xs[t], pre, trace=trace)
             torch.cuda.current_stream().synchronize()
             if t >= args.offload_warmup:
                 step_s.append(time.perf_counter() - t1)
+        # spot check of the last step (outside the timing): every layer's output read from the
+        # slots equals the resident layer's, bit for bit
+        spot = all(torch.equal(outs[l], ops.moe_layer(xs[n_tok - 1], ly.router_w, ly.experts,
+                                                      top_k=K, logit_bias=ly.logit_bias,
+                                                      path="decode"))
+                   for l, ly in enumerate(layers))
         torch.cuda.synchronize()
         st = fresh.stats()
         diff = {k2: st[k2] - base[k2] for k2 in st if k2 not in ("capacity", "resident_count",
@@ -603,10 +609,17 @@ def offload_bench(layers, args, dev) -> dict:
                               / max(diff["demand_count"], 1),
             "h2d_GBps": (diff["prefetch_bytes"] + diff["demand_bytes"]) / total / 1e9,
             "counters": diff,
+            "last_step_equals_resident_layers": bool(spot),
+            "reference_semantics": ready_time_replay(trace, L * args.offload_slots,
+                                                     calib["eight_experts_us_per_expert"]["p50"],
+                                                     args.offload_warmup * L),
         }
+        rs = runs[name]["reference_semantics"]
         log(f"[bench] offload {name}: TPOT {runs[name]['tpot_ms_mean']:.2f} ms, hit rate "
             f"{100 * runs[name]['hit_rate']:.1f}% (ready in time {100 * runs[name]['ready_hit_rate']:.1f}%, "
-            f"{diff['ready_late_miss_count']} ready-late), H2D {runs[name]['h2d_GBps']:.1f} GB/s")
+            f"{diff['ready_late_miss_count']} ready-late), H2D {runs[name]['h2d_GBps']:.1f} GB/s; "
+            f"ReadyTimeExpertCacheManager replay: hit rate {100 * rs['hit_rate']:.1f}%, "
+            f"{rs['ready_late_miss_count']} ready-late misses")
     pool.close()
     del pool
     return {
@@ -619,6 +632,36 @@ def offload_bench(layers, args, dev) -> dict:
         "runs": runs,
         "h2d_calibration": calib,
     }
+
+
+def ready_time_replay(trace, capacity: int, service_us: float, skip: int) -> dict:
+    """The offload run's call sequence (per layer call: demanded ids, then the prefetch list, at
+    the host time the call made them) through the reference's ReadyTimeExpertCacheManager
+    (cache_manager.py:298-578, native): one LRU of `capacity` keys, each issue a transfer of
+    `service_us` (the measured pinned H2D time per expert), batches of one, no deadline. A
+    demand then hits only experts whose virtual transfer completed by its arrival; a demand of
+    one still in flight is a ready-late miss. Counters cover the calls after the first `skip`
+    (the warmup steps), as the measured counters do."""
+    from mtp_amd.cache_manager import ReadyTimeExpertCacheManager
+    m = ReadyTimeExpertCacheManager(capacity=capacity, service_us_per_issue=service_us)
+    t0 = trace[0][3] if trace else 0.0
+    base = None
+    for i, (layer, ids, pre, t_us) in enumerate(trace):
+        if i == skip:
+            base = m.snapshot().as_dict()
+        m.demand_many(layer, ids, arrival_us=t_us - t0)
+        m.issue_prefetches(layer, pre, arrival_us=t_us - t0)
+    m.finish()
+    s = m.snapshot().as_dict()
+    base = base or {k: 0 for k in s}
+    keys = ("issued_fetch_count", "used_fetch_count", "demand_count", "demand_hit_count",
+            "demand_miss_count", "evicted_before_use_count", "ready_late_miss_count",
+            "late_completion_unused_count")
+    d = {k: int(s[k] - base[k]) for k in keys}
+    d["hit_rate"] = d["demand_hit_count"] / max(d["demand_count"], 1)
+    d.update({"capacity": capacity, "service_us_per_issue": service_us,
+              "arrival": "host time of each layer call (demand, then the prefetch list)"})
+    return d
 
 
 def h2d_calibration(pool, reps: int = 200) -> dict:

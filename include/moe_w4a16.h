@@ -395,6 +395,72 @@ int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32
                          const int32_t* prefetch, int32_t n_prefetch, int32_t path, void* stream,
                          int32_t* hits);
 
+/* ---- Cache accounting on virtual time (host only: no HIP call, no payload bytes).
+ * The reference's cache-lab managers for a trace of prefetch issues and demands with arrival
+ * times (microseconds, nondecreasing for meaningful queue timing). Keys are (layer, expert);
+ * one LRU of `capacity` keys over all layers, as in the reference.
+ *   MOE_READY_CACHE_CONTROLLED: ControlledExpertCacheManager (cache_manager.py:208-279): a
+ *     prefetch of a missing key enters the LRU at once; arrival times are ignored.
+ *   MOE_READY_CACHE_READY_TIME: ReadyTimeExpertCacheManager (cache_manager.py:298-578): issues
+ *     are served in batches of queue_batch_size by one server (service_us_per_batch +
+ *     service_us_per_issue per issue, a partial batch released queue_deadline_us after its first
+ *     issue or at finish); a transfer's key enters the LRU at its completion time; a demand hits
+ *     only keys completed by arrival + queue_deadline_us; a demand of an in-flight key is a miss
+ *     and a ready-late miss, and that transfer's completion counts as a late completion left
+ *     unused.
+ * Non-finite service times or deadline are refused (MOE_ERR_SHAPE, the reference's ValueError);
+ * negative ones are clamped to 0 and a batch size below 1 to 1. Not thread-safe. */
+enum { MOE_READY_CACHE_CONTROLLED = 0, MOE_READY_CACHE_READY_TIME = 1 };
+
+/* Counters of CacheManagerSnapshot / ReadyTimeCacheManagerSnapshot (cache_manager.py:192-205,
+ * 282-295), same names and meaning. */
+typedef struct moe_ready_cache_snapshot_v1 {
+  int64_t capacity;
+  int64_t resident_count;
+  int64_t issued_fetch_count;
+  int64_t used_fetch_count;
+  int64_t unused_fetch_count; /* resident unused prefetches + late completions left unused */
+  int64_t demand_count;
+  int64_t demand_hit_count;
+  int64_t demand_miss_count;
+  int64_t evicted_before_use_count;
+  int64_t ready_late_miss_count;
+  int64_t late_completion_unused_count;
+  int64_t queue_batch_count;
+  double queue_service_us;
+  double queue_total_span_us;
+  double queue_wait_us;
+  double queue_max_delay_us;
+  double queue_event_interval_us;
+  double queue_deadline_us;
+  int64_t queue_batch_size;
+} moe_ready_cache_snapshot_v1;
+
+/* Replaces the managers' constructors (cache_manager.py:211-219, 309-354). */
+int moe_ready_cache_create_v1(int32_t mode, int64_t capacity, double service_us_per_issue,
+                              double service_us_per_batch, int64_t queue_batch_size,
+                              double queue_deadline_us, uint64_t* handle);
+int moe_ready_cache_destroy_v1(uint64_t handle);
+
+/* issue_prefetch of each expert of `experts` (host int32 [n]) in order at one arrival time
+ * (cache_manager.py:221-230, 356-378; issue_prefetches :380-397). issued_flags: NULL or host
+ * int32 [n] (1 = a new transfer); issued: NULL or the count. */
+int moe_ready_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* experts,
+                                int32_t n, double arrival_us, int32_t* issued_flags,
+                                int32_t* issued);
+
+/* demand of each expert in order at one arrival time (cache_manager.py:232-247, 399-425).
+ * hit_flags: NULL or host int32 [n]; hits: NULL or the count. */
+int moe_ready_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                              double arrival_us, int32_t* hit_flags, int32_t* hits);
+
+/* advance_to (cache_manager.py:427-433) and finish (:435-453); no-ops for CONTROLLED. */
+int moe_ready_cache_advance_v1(uint64_t handle, double arrival_us);
+int moe_ready_cache_finish_v1(uint64_t handle);
+
+/* snapshot (cache_manager.py:249-262, 455-485). */
+int moe_ready_cache_stats_v1(uint64_t handle, moe_ready_cache_snapshot_v1* out);
+
 #ifdef __cplusplus
 }
 #endif

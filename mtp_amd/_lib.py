@@ -59,6 +59,13 @@ EXPORTED = (
     "moe_slot_cache_stats_v1",
     "moe_slot_cache_slot_of_v1",
     "moe_offload_layer_v1",
+    "moe_ready_cache_create_v1",
+    "moe_ready_cache_destroy_v1",
+    "moe_ready_cache_prefetch_v1",
+    "moe_ready_cache_demand_v1",
+    "moe_ready_cache_advance_v1",
+    "moe_ready_cache_finish_v1",
+    "moe_ready_cache_stats_v1",
 )
 
 
@@ -83,6 +90,16 @@ class SlotCacheCounters(ctypes.Structure):
         "unused_fetch_count", "demand_count", "demand_hit_count", "demand_miss_count",
         "evicted_before_use_count", "prefetch_bytes", "demand_bytes",
         "prefetch_skipped_pinned_count", "ready_late_miss_count", "ready_late_wait_ns")]
+
+
+class ReadyCacheStats(ctypes.Structure):
+    _fields_ = [(name, c_int64) for name in (
+        "capacity", "resident_count", "issued_fetch_count", "used_fetch_count",
+        "unused_fetch_count", "demand_count", "demand_hit_count", "demand_miss_count",
+        "evicted_before_use_count", "ready_late_miss_count", "late_completion_unused_count",
+        "queue_batch_count")] + [(name, ctypes.c_double) for name in (
+        "queue_service_us", "queue_total_span_us", "queue_wait_us", "queue_max_delay_us",
+        "queue_event_interval_us", "queue_deadline_us")] + [("queue_batch_size", c_int64)]
 
 
 class HrPredictorParams(ctypes.Structure):
@@ -168,6 +185,16 @@ _SIGS = {
         [ctypes.c_uint64, _I, _P, _I, _P, _P, _I, POINTER(ExpertSet), _P, c_int64, _P, _P, _P, _I,
          _I, _P, POINTER(c_int32)],
         c_int32),
+    "moe_ready_cache_create_v1": ([_I, c_int64, ctypes.c_double, ctypes.c_double, c_int64,
+                                   ctypes.c_double, POINTER(ctypes.c_uint64)], c_int32),
+    "moe_ready_cache_destroy_v1": ([ctypes.c_uint64], c_int32),
+    "moe_ready_cache_prefetch_v1": ([ctypes.c_uint64, _I, _P, _I, ctypes.c_double, _P,
+                                     POINTER(c_int32)], c_int32),
+    "moe_ready_cache_demand_v1": ([ctypes.c_uint64, _I, _P, _I, ctypes.c_double, _P,
+                                   POINTER(c_int32)], c_int32),
+    "moe_ready_cache_advance_v1": ([ctypes.c_uint64, ctypes.c_double], c_int32),
+    "moe_ready_cache_finish_v1": ([ctypes.c_uint64], c_int32),
+    "moe_ready_cache_stats_v1": ([ctypes.c_uint64, POINTER(ReadyCacheStats)], c_int32),
 }
 
 

@@ -19,6 +19,7 @@ with expert_stride_bytes = blob size and expert_row = the layer's expert -> slot
 from __future__ import annotations
 
 import ctypes
+import time
 from dataclasses import dataclass
 
 import torch
@@ -410,8 +411,14 @@ class OffloadDecoder:
         torch.cuda.current_stream().synchronize()
         return [list(dict.fromkeys(self._pred_host[l].reshape(-1).tolist())) for l in range(L)]
 
-    def step(self, x: torch.Tensor, prefetch: list[list[int]] | None = None) -> list[torch.Tensor]:
-        """One decode step over every layer; `prefetch[l]` is issued right after layer l."""
+    def step(self, x: torch.Tensor, prefetch: list[list[int]] | None = None,
+             trace: list | None = None) -> list[torch.Tensor]:
+        """One decode step over every layer; `prefetch[l]` is issued right after layer l.
+
+        trace: if given, one (layer, demanded experts, prefetched experts, host time in us)
+        record per layer call is appended (the call's demand and prefetch happen inside it, after
+        the routed ids reached the host), so the sequence can be replayed through the
+        reference's virtual-time managers (mtp_amd.cache_manager)."""
         T = x.shape[0]
         need = ops.workspace_bytes(T, self.top_k, self.pool.layer_experts(0), False, self.path)
         if self._ws is None or self._ws.numel() < need:
@@ -423,4 +430,8 @@ class OffloadDecoder:
                                                path=self.path, workspace=self._ws,
                                                prefetch=prefetch[l] if prefetch is not None else None)
             outs.append(out)
+            if trace is not None:
+                trace.append((l, self._ids_host.reshape(-1).tolist(),
+                              list(prefetch[l]) if prefetch is not None else [],
+                              time.perf_counter() * 1e6))
         return outs

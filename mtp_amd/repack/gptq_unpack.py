@@ -216,7 +216,7 @@ def load_repacked_projection_tensors(store: RepackedMoeExpertStore, *, layer: in
 def dequantize_repacked_projection(store: RepackedMoeExpertStore, *, layer: int, expert: int,
                                    projection: str, bits: int = 4,
                                    dtype: str | torch.dtype = torch.bfloat16,
-                                   device: str | torch.device = "cuda") -> torch.Tensor:
+                                   device: str | torch.device = "cpu") -> torch.Tensor:
     tensors = load_repacked_projection_tensors(store, layer=layer, expert=expert,
                                                projection=projection, device=device)
     return dequantize_gptq_projection(tensors, bits=bits, dtype=dtype)
@@ -228,7 +228,7 @@ def apply_dequantized_projection(input_tensor: torch.Tensor, weight: torch.Tenso
 
 def load_single_expert_weights(store: RepackedMoeExpertStore, *, layer: int, expert: int,
                                bits: int = 4, dtype: str | torch.dtype = torch.bfloat16,
-                               device: str | torch.device = "cuda") -> SingleExpertWeights:
+                               device: str | torch.device = "cpu") -> SingleExpertWeights:
     """Dense dequantised weights of one expert (HIP dequant kernel)."""
     projs = {p: dequantize_repacked_projection(store, layer=layer, expert=expert, projection=p,
                                                bits=bits, dtype=dtype, device=device)
@@ -279,11 +279,13 @@ class _Int4ExpertStack(torch.nn.Module):
         self.group_size = int(group)
         self._view: MoeExperts | None = None
         self._dense: dict = {}
+        self._staged: dict = {}
 
     def _apply(self, fn, recurse=True):
         out = super()._apply(fn, recurse)
         self._view = None
         self._dense = {}
+        self._staged = {}
         return out
 
     def _stack_of(self, proj: str) -> GptqStack:
@@ -298,15 +300,48 @@ class _Int4ExpertStack(torch.nn.Module):
             self._view = view
         return self._view
 
+    def _kernel_device(self, input_device: torch.device | None = None) -> torch.device:
+        """Where the kernels run: the input's ROCm device, else the module's, else the current
+        one (a host module and host inputs run there and return on the host, as the reference's
+        CPU modules do; there is no CPU path)."""
+        if input_device is not None and input_device.type == "cuda":
+            return input_device
+        home = self.gate_proj_qweight.device
+        if home.type == "cuda":
+            return home
+        if not torch.cuda.is_available():
+            raise RuntimeError("the W4A16 expert kernels run on a ROCm device and none is "
+                               "available; there is no CPU fallback")
+        return torch.device("cuda", torch.cuda.current_device())
+
+    def _kernel_experts(self, dev: torch.device) -> MoeExperts:
+        """The int4 stacks on ROCm device ``dev``: the module's buffers when they live there,
+        else a copy staged once per device (dropped when the module moves)."""
+        view = self.int4_experts()
+        if view.device == dev:
+            return view
+        staged = self._staged.get(dev)
+        if staged is None:
+            staged = MoeExperts(view.gate.to(dev), view.up.to(dev), view.down.to(dev),
+                                view.group_size)
+            staged._validated = True
+            self._staged[dev] = staged
+        return staged
+
     def _dequantized(self, proj: str, row: int = 0) -> torch.Tensor:
         """Dense Linear-orientation weight of one projection of stack row ``row`` in the
-        module's dtype, dequantised bit-exactly by the HIP kernel on first use."""
+        module's dtype, dequantised bit-exactly by the HIP kernel on first use and kept on the
+        module's device."""
         key = (proj, row)
         if key not in self._dense:
-            st = self._stack_of(proj)
-            self._dense[key] = ops.dequantize(st.qweight[row], st.qzeros[row], st.scales[row],
-                                              group_size=self.group_size, linear_weight=True,
-                                              dtype=self.compute_dtype)
+            home = self.gate_proj_qweight.device
+            dev = self._kernel_device()
+            st = getattr(self._kernel_experts(dev), {"gate_proj": "gate", "up_proj": "up",
+                                                      "down_proj": "down"}[proj])
+            w = ops.dequantize(st.qweight[row], st.qzeros[row], st.scales[row],
+                               group_size=self.group_size, linear_weight=True,
+                               dtype=self.compute_dtype)
+            self._dense[key] = w if home.type == "cuda" else w.to(home)
         return self._dense[key]
 
     @property
@@ -326,21 +361,21 @@ class _Int4ExpertStack(torch.nn.Module):
             raise ValueError(msg)
         if input_tensor.dtype not in ops.OUT_DTYPES:
             raise TypeError(f"input dtype {input_tensor.dtype} is not one of bf16/fp16/fp32")
-        experts = self.int4_experts()
-        if input_tensor.device != experts.device:
-            msg = (f"input on {input_tensor.device}, expert weights on {experts.device}; the "
-                   "W4A16 kernels run on a ROCm device (move the module with .to('cuda'))")
-            raise ValueError(msg)
-        x = input_tensor.reshape(-1, self.hidden_size).to(torch.bfloat16).contiguous()
+        # Host modules or host inputs (the reference's device="cpu" default) are staged to the
+        # ROCm device the kernels run on; the result returns on the input's device.
+        home = input_tensor.device
+        dev = self._kernel_device(home)
+        experts = self._kernel_experts(dev)
+        x = input_tensor.reshape(-1, self.hidden_size).to(device=dev, dtype=torch.bfloat16)
+        x = x.contiguous()
         T, k = x.shape[0], len(rows)
-        dev = x.device
         ids = torch.tensor(rows, dtype=torch.int32, device=dev).expand(T, k).contiguous()
         if weights is None:
             w = torch.ones(T, k, dtype=torch.float32, device=dev)
         else:
-            w = weights.to(torch.float32).expand(T, k).contiguous()
+            w = weights.to(device=dev, dtype=torch.float32).expand(T, k).contiguous()
         out = ops.fused_experts(x, ids, w, experts)
-        return out.to(input_tensor.dtype).reshape(input_tensor.shape)
+        return out.to(device=home, dtype=input_tensor.dtype).reshape(input_tensor.shape)
 
 
 class SingleExpertMlp(_Int4ExpertStack):
@@ -457,7 +492,7 @@ class TopKExpertMlp(_Int4ExpertStack):
 
 
 def load_quantized_expert(store: RepackedMoeExpertStore, *, layer: int, expert: int,
-                          device: str | torch.device = "cuda") -> QuantizedExpertWeights:
+                          device: str | torch.device = "cpu") -> QuantizedExpertWeights:
     projs = {p: load_repacked_projection_tensors(store, layer=layer, expert=expert, projection=p,
                                                  device=device)
              for p in ("gate_proj", "up_proj", "down_proj")}
@@ -473,7 +508,7 @@ def _check_bits(bits: int) -> None:
 
 def load_single_expert_mlp(store: RepackedMoeExpertStore, *, layer: int, expert: int,
                            bits: int = 4, dtype: str | torch.dtype = torch.bfloat16,
-                           device: str | torch.device = "cuda") -> SingleExpertMlp:
+                           device: str | torch.device = "cpu") -> SingleExpertMlp:
     _check_bits(bits)
     return SingleExpertMlp(load_quantized_expert(store, layer=layer, expert=expert, device=device),
                            dtype=dtype)
@@ -482,7 +517,7 @@ def load_single_expert_mlp(store: RepackedMoeExpertStore, *, layer: int, expert:
 def load_topk_expert_mlp(store: RepackedMoeExpertStore, *, layer: int,
                          expert_ids: list[int] | tuple[int, ...], bits: int = 4,
                          dtype: str | torch.dtype = torch.bfloat16,
-                         device: str | torch.device = "cuda") -> TopKExpertMlp:
+                         device: str | torch.device = "cpu") -> TopKExpertMlp:
     _check_bits(bits)
     unique_expert_ids = tuple(dict.fromkeys(int(expert_id) for expert_id in expert_ids))
     experts = {eid: load_quantized_expert(store, layer=layer, expert=eid, device=device)

@@ -57,12 +57,15 @@ def test_module_moves_rebuild_the_kernel_view():
     assert mlp.int4_experts().gate.qweight.data_ptr() == mlp.gate_proj_qweight.data_ptr()
 
 
-def test_forward_on_host_tensors_fails_loudly():
+def test_forward_without_a_rocm_device_fails_loudly(monkeypatch):
+    """Host modules and inputs are staged to a ROCm device; with none available the forward
+    raises (there is no CPU path), and shape errors come first, as in the reference."""
     mlp = SingleExpertMlp(_quantized(2))
-    with pytest.raises(ValueError, match="ROCm"):
-        mlp(torch.zeros(1, H, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="last dim"):
         mlp(torch.zeros(1, H + 8, dtype=torch.bfloat16))
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        mlp(torch.zeros(1, H, dtype=torch.bfloat16))
 
 
 def test_dense_single_expert_weights_are_refused_with_a_message():

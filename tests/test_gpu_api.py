@@ -119,11 +119,13 @@ def test_topk_harness_call_sequence(store_dir, dtype_name):
     err = moe_ref.rel_err(out.reshape(6, H).float().cpu().numpy(), ref)
     print(f"  {dtype_name}: rel_err={err:.3e}", flush=True)
     assert err <= LAYER_RTOL
-    # the same module moved to the CPU and back runs again from its buffers
+    # the same module moved to the CPU runs from its host buffers (staged to the GPU, result on
+    # the host, same bits), and moved back runs again from its buffers
     mlp.to("cpu")
     assert next(mlp.buffers()).device.type == "cpu"
-    with pytest.raises(ValueError):
-        mlp(x.cpu(), ids, weights.cpu())
+    with torch.inference_mode():
+        on_host = mlp(x.cpu(), ids, weights.cpu())
+    assert on_host.device.type == "cpu" and torch.equal(on_host, out.cpu())
     mlp.to(device)
     with torch.inference_mode():
         again = mlp(x, ids, weights)
@@ -219,3 +221,51 @@ def test_trace_harness_call_sequence(store_dir, tmp_path, dtype_name, mode):
     err = moe_ref.rel_err(out.reshape(1, H).float().cpu().numpy(), ref)
     print(f"  trace {dtype_name}/{mode}: rel_err={err:.3e}", flush=True)
     assert err <= LAYER_RTOL
+
+
+@pytest.mark.parametrize("dtype_name", ["bf16", "fp32"])
+def test_harness_call_sequences_on_the_reference_default_device(store_dir, dtype_name):
+    """The reference's harnesses run with --device cpu by default (smoke_topk_expert_mlp.py:58,
+    smoke_single_expert_mlp.py:36) and its loaders default to device="cpu"
+    (gptq_unpack.py:337, 357): the modules then hold host tensors, the device probe finds the
+    CPU, inputs are drawn there, and the outputs come back there. The kernels run on the GPU
+    (host tensors staged); the results equal the oracle's and the GPU-resident module's bits."""
+    from mtp_amd.repack import resolve_torch_dtype
+    d, ex = store_dir
+    target = resolve_torch_dtype(dtype_name)
+    expert_ids = [4, 0, 7, 4]
+    torch.manual_seed(1)
+    with RepackedMoeExpertStore(d) as store:
+        mlp = load_topk_expert_mlp(store, layer=0, expert_ids=expert_ids, bits=4, dtype=target)
+        single = load_single_expert_mlp(store, layer=0, expert=2, bits=4, dtype=target)
+    device = next(mlp.parameters(), next(mlp.buffers())).device
+    assert device.type == "cpu"
+    x = torch.randn(2, 3, mlp.hidden_size, device=device, dtype=target)
+    ids = torch.tensor(expert_ids, dtype=torch.long)
+    weights = torch.tensor([0.4, 0.3, 0.2, 0.1], dtype=target, device=device)
+    with torch.inference_mode():
+        out = mlp(x, ids, weights)
+    assert out.device.type == "cpu" and out.shape == x.shape and out.dtype == target
+    xb = x.reshape(6, H).to(torch.bfloat16)
+    ref = moe_ref.moe_layer_f32(bf16_bits(xb), np.tile(np.array(expert_ids, np.int32), (6, 1)),
+                                np.tile(weights.float().numpy(), (6, 1)), experts_to_np(ex))
+    err = moe_ref.rel_err(out.reshape(6, H).float().numpy(), ref)
+    print(f"  host top-k {dtype_name}: rel_err={err:.3e}", flush=True)
+    assert err <= LAYER_RTOL
+    gpu_out = mlp.to("cuda")(x.cuda(), ids, weights.cuda())
+    assert torch.equal(gpu_out.cpu(), out)
+    # single expert: inputs on mlp.gate_proj.device (the host), dense views bit-exact there
+    assert single.gate_proj.device.type == "cpu" and single.gate_proj.dtype == target
+    xs = torch.randn(2, 4, single.hidden_size, device=single.gate_proj.device,
+                     dtype=single.gate_proj.dtype)
+    with torch.inference_mode():
+        ys = single(xs)
+    assert ys.device.type == "cpu" and ys.shape == xs.shape
+    want = gptq_ref.dequant_f32(ex.gate.qweight[2].numpy(), ex.gate.qzeros[2].numpy(),
+                                f16_bits(ex.gate.scales[2]))
+    assert np.array_equal(single.gate_proj.float().numpy(),
+                          torch.from_numpy(want).to(target).float().numpy())
+    xb = xs.reshape(8, H).to(torch.bfloat16)
+    ref = moe_ref.moe_layer_f32(bf16_bits(xb), np.full((8, 1), 2, np.int32),
+                                np.ones((8, 1), np.float32), experts_to_np(ex))
+    assert moe_ref.rel_err(ys.reshape(8, H).float().numpy(), ref) <= LAYER_RTOL

@@ -417,3 +417,65 @@ def test_ready_late_first_demands_are_counted_from_event_times():
         assert st["demand_hit_count"] == 8
     finally:
         pool.close()
+
+
+def test_offload_decoder_at_the_full_config5_shape():
+    """Config 5's loop at its own shape: two offloaded layers of H 2048 / I 512 / 256 experts
+    with 64 HBM slots each, OffloadDecoder.step at batch 1 for several steps with predicted
+    prefetch lists (the hidden-residual predictor) after every layer. Every step's per-layer
+    output equals the resident layer's bit for bit, and the slot cache's counters equal one
+    LRU oracle per layer (cache_manager.py:208-279) fed the same demanded ids and prefetch lists
+    (prefetches follow layer_done, so no slot is pinned when they run)."""
+    from mtp_amd.offload import OffloadDecoder
+    from mtp_amd.predictor import HiddenResidualExpertPredictor
+    from oracle.cache_ref import LruCounters
+    L, E, H, I, K, S = 2, 256, 2048, 512, 8, 64
+    _say("config 5 full shape: building 2 layers")
+    layers = [synth.make_layer(l, zipf=True, device="cuda") for l in range(L)]
+    pool = OffloadedExperts(L, E, H, I, S, group_size=128, device="cuda")
+    try:
+        for l, g in enumerate(layers):
+            pool.store_layer(l, g.experts)
+        torch.cuda.synchronize()
+        hr = HiddenResidualExpertPredictor(hidden_size=H, num_experts=E, num_layers=L, seed=9,
+                                           device="cuda")
+        dec = OffloadDecoder(pool, [g.router_w for g in layers], [g.logit_bias for g in layers],
+                             top_k=K, predictor=hr, prefetch_k=16, path="decode")
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(17)
+        xs = torch.randn(7, 1, H, generator=gen, device="cuda").to(torch.bfloat16)
+        trace = []
+        for t in range(6):
+            _say(f"  step {t}")
+            pre = dec.predict(xs[t + 1])
+            outs = dec.step(xs[t], pre, trace=trace)
+            for l, g in enumerate(layers):
+                want = ops.moe_layer(xs[t], g.router_w, g.experts, top_k=K,
+                                     logit_bias=g.logit_bias, path="decode")
+                torch.cuda.synchronize()
+                assert torch.equal(outs[l], want), (t, l)
+        oracles = [LruCounters(S) for _ in range(L)]
+        for layer, ids, pre, _ in trace:
+            for e in ids:
+                oracles[layer].demand(layer, e)
+            for e in pre:
+                oracles[layer].issue_prefetch(layer, e)
+        st = pool.stats()
+        want = {
+            "issued_fetch_count": sum(o.issued for o in oracles),
+            "used_fetch_count": sum(o.used for o in oracles),
+            "unused_fetch_count": sum(o.unused() for o in oracles),
+            "demand_count": sum(o.demand_count for o in oracles),
+            "demand_hit_count": sum(o.hits for o in oracles),
+            "demand_miss_count": sum(o.misses for o in oracles),
+            "evicted_before_use_count": sum(o.evicted_before_use for o in oracles),
+            "resident_count": sum(len(o.cache) for o in oracles),
+        }
+        for k, v in want.items():
+            assert st[k] == v, (k, st[k], v)
+        assert st["prefetch_skipped_pinned_count"] == 0
+        assert st["demand_count"] == 6 * L * K and st["issued_fetch_count"] > 0
+        _say(f"  hits {st['demand_hit_count']} of {st['demand_count']}, issued "
+             f"{st['issued_fetch_count']}")
+    finally:
+        pool.close()
