@@ -382,8 +382,10 @@ int moe_slot_cache_slot_of_v1(uint64_t handle, int32_t layer, int32_t expert);
 /* One offloaded MoE layer of a decode step in one call: router logits and top-k into the
  * workspace, the routed ids to ids_host (pinned host, T * top_k; the call waits for them on
  * stream), moe_slot_cache_demand_v1, the routed experts from the layer's slots (experts = the
- * layer's slot view, as for moe_fused_experts_v1), moe_slot_cache_layer_done_v1 and, when
- * n_prefetch > 0, moe_slot_cache_prefetch_v1 of the host list prefetch. Replaces the per-layer
+ * layer's slot view, as for moe_fused_experts_v1), when n_prefetch > 0 the prefetch of the host
+ * list prefetch (as moe_slot_cache_prefetch_v1, with the demand's slots still pinned and without
+ * the copy streams' wait for the compute stream, which the ids' wait has already drained), then
+ * moe_slot_cache_layer_done_v1. Replaces the per-layer
  * sequence of the reference's offloaded decode (router top-k, then
  * ControlledExpertCacheManager.demand, cache_manager.py:233-247, then the expert MLPs, then
  * issue_prefetch, :222-231) with one host call. Workspace as moe_layer_v1 (no shared expert).

@@ -10,6 +10,12 @@
 constexpr int kErrorBufferBytes = 512;
 char* moe_error_buffer();
 
+// Slot-cache prefetch for moe_offload_layer_v1 (slot_cache.hip): no ordering wait on the compute
+// stream; the caller has synchronised that stream after every kernel reading an unpinned slot of
+// the layer was enqueued, and the latest demand's slots are still pinned.
+int slot_cache_prefetch_synced(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                               void* compute_stream);
+
 // Argument checks of a routed layer call that involve no workspace (api.hip): 0 or the error
 // code moe_layer_v1 returns for the same input (message in moe_error_buffer).
 int check_layer_args(const uint16_t* x, int32_t T, const uint16_t* router_w, int32_t top_k,

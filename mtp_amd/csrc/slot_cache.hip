@@ -74,10 +74,13 @@ struct ReadyCheck {
 struct Layer {
   std::vector<Slot> slots;
   std::vector<int> slot_of;   // expert -> slot or -1
-  // per copy stream: prefetch copies not yet waited for by the compute stream, and the event
-  // after the layer's latest prefetch copies on that stream
+  // per copy stream: prefetch copies not yet waited for by the compute stream, and the prefetch
+  // call whose timing event follows the layer's latest copies on that stream (its event
+  // pf_ev[(seq % kEventRing) * kCopyStreams + stream] is also what a demand waits on; if the
+  // ring slot has been re-recorded since, the later record on the same stream completes after
+  // these copies, so the wait stays correct)
   bool pending[kCopyStreams] = {};
-  hipEvent_t prefetch_done[kCopyStreams] = {};
+  uint64_t done_seq[kCopyStreams] = {};
 };
 
 struct Cache {
@@ -215,9 +218,6 @@ int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handl
     for (hipStream_t& st : c->side)
       SC_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "create copy stream");
     SC_HIP(hipEventCreateWithFlags(&c->compute_mark, hipEventDisableTiming), "create event");
-    for (Layer& L : c->layers)
-      for (hipEvent_t& e : L.prefetch_done)
-        SC_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "create event");
     SC_HIP(hipHostMalloc((void**)&c->staging, (size_t)kStagingRing * d.num_experts * 4,
                          hipHostMallocDefault), "pinned staging");
     c->staging_done.assign(kStagingRing, nullptr);
@@ -238,8 +238,6 @@ int moe_slot_cache_destroy_v1(uint64_t handle) {
   if (live(c)) {
     hipSetDevice(c->d.device);
     for (hipStream_t st : c->side) hipStreamSynchronize(st);
-    for (Layer& L : c->layers)
-      for (hipEvent_t e : L.prefetch_done) hipEventDestroy(e);
     for (hipEvent_t e : c->staging_done) hipEventDestroy(e);
     for (hipEvent_t e : c->pf_ev) hipEventDestroy(e);
     for (hipEvent_t e : c->dm_ev) hipEventDestroy(e);
@@ -252,10 +250,16 @@ int moe_slot_cache_destroy_v1(uint64_t handle) {
   return MOE_OK;
 }
 
-int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
-                               void* compute_stream, int32_t* issued) {
-  Cache* c = from_handle(handle);
-  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+}  // extern "C"
+
+namespace {
+
+// The prefetch of moe_slot_cache_prefetch_v1. order_after_compute: make the copy streams wait
+// for the work already on the compute stream first (an evicted slot may still be read by an
+// enqueued kernel). Without it the caller guarantees that every kernel reading an unpinned slot
+// of the layer has completed (see slot_cache_prefetch_synced).
+int prefetch_impl(Cache* c, int32_t layer, const int32_t* experts, int32_t n,
+                  void* compute_stream, int32_t* issued, bool order_after_compute) {
   if (layer < 0 || layer >= c->d.num_layers || n < 0 || (n > 0 && !experts))
     return fail(MOE_ERR_SHAPE, "slot cache prefetch: bad layer or list");
   for (int i = 0; i < n; ++i)
@@ -263,7 +267,7 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
       return fail(MOE_ERR_SHAPE, "slot cache: expert id out of range");
   Layer& L = c->layers[layer];
   int count = 0;
-  bool ordered = false;
+  bool ordered = !order_after_compute;
   bool used[kCopyStreams] = {};
   for (int i = 0; i < n; ++i) {
     const int e = experts[i];
@@ -306,14 +310,37 @@ int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* ex
     if (rc) return rc;
     for (int k = 0; k < kCopyStreams; ++k) {
       if (!used[k]) continue;
-      SC_HIP(hipEventRecord(L.prefetch_done[k], c->side[k]), "record prefetch done");
       L.pending[k] = true;
+      L.done_seq[k] = seq;
       SC_HIP(hipEventRecord(c->pf_ev[(seq % kEventRing) * kCopyStreams + k], c->side[k]),
-             "record prefetch time");
+             "record prefetch done");
     }
   }
   if (issued) *issued = count;
   return MOE_OK;
+}
+
+}  // namespace
+
+// Prefetch for a caller that synchronised the compute stream after enqueueing every kernel
+// that reads the layer's slots, except the kernels of the layer's latest demand, whose slots
+// must still be pinned (moe_offload_layer_v1: the routed ids' wait drains the stream, then the
+// demand pins its slots and the layer's kernels are enqueued). No unpinned slot can then be
+// read by pending work, so the copies need no ordering wait on the compute stream.
+int slot_cache_prefetch_synced(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                               void* compute_stream) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  return prefetch_impl(c, layer, experts, n, compute_stream, nullptr, false);
+}
+
+extern "C" {
+
+int moe_slot_cache_prefetch_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
+                               void* compute_stream, int32_t* issued) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  return prefetch_impl(c, layer, experts, n, compute_stream, issued, true);
 }
 
 int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
@@ -349,7 +376,8 @@ int moe_slot_cache_demand_v1(uint64_t handle, int32_t layer, const int32_t* expe
   }
   for (int k = 0; k < kCopyStreams; ++k) {
     if (!L.pending[k] || !live(c)) continue;
-    SC_HIP(hipStreamWaitEvent(cs, L.prefetch_done[k], 0), "compute waits prefetch");
+    SC_HIP(hipStreamWaitEvent(cs, c->pf_ev[(L.done_seq[k] % kEventRing) * kCopyStreams + k], 0),
+           "compute waits prefetch");
     L.pending[k] = false;
   }
   int nh = 0;
