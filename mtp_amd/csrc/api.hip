@@ -674,11 +674,28 @@ int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32
   const int n = T * top_k;
   MOE_CHECK_HIP(launch_router_logits(x, T, experts->hidden, router_w, E, nullptr, logit_bias,
                                      logits, s), "offload layer: router logits");
-  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, 0, ids, w, s),
+  // The host-managed cache needs the routed ids: the one wait of the layer. Pinned host memory
+  // that HIP maps at the same address on the device (hipHostMalloc's) takes them straight from
+  // the top-k kernel's lanes, with no copy on the stream; both ends of the range must map, at
+  // their own addresses. Other host memory gets a copy.
+  int32_t* mirror = nullptr;
+  {
+    void* d0 = nullptr;
+    void* d1 = nullptr;
+    const bool mapped =
+        hipHostGetDevicePointer(&d0, ids_host, 0) == hipSuccess && d0 == (void*)ids_host &&
+        hipHostGetDevicePointer(&d1, ids_host + (n - 1), 0) == hipSuccess &&
+        d1 == (void*)(ids_host + (n - 1));
+    if (mapped)
+      mirror = ids_host;
+    else
+      (void)hipGetLastError();  // a failed lookup must not surface at the next launch check
+  }
+  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, 0, ids, w, s, mirror),
                 "offload layer: router topk");
-  // the host-managed cache needs the routed ids: the one wait of the layer
-  MOE_CHECK_HIP(hipMemcpyAsync(ids_host, ids, (size_t)n * 4, hipMemcpyDeviceToHost, s),
-                "offload layer: ids to the host");
+  if (!mirror)
+    MOE_CHECK_HIP(hipMemcpyAsync(ids_host, ids, (size_t)n * 4, hipMemcpyDeviceToHost, s),
+                  "offload layer: ids to the host");
   MOE_CHECK_HIP(hipStreamSynchronize(s), "offload layer: wait for the ids");
   rc = moe_slot_cache_demand_v1(cache, layer, ids_host, n, stream, hits);
   if (rc) return rc;

@@ -32,8 +32,11 @@ hipError_t launch_dequant(const ProjDev& p, const int32_t* g_idx, int E, int K, 
 hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t* W, int E,
                                 const uint16_t* shared_w, const float* bias, float* logits,
                                 hipStream_t stream);
+// ids_mirror: optional second destination of the ids (e.g. pinned host memory mapped into the
+// device's address space), written by the same lanes as ids.
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
-                              int32_t* ids, float* weights, hipStream_t stream);
+                              int32_t* ids, float* weights, hipStream_t stream,
+                              int32_t* ids_mirror = nullptr);
 // Prefill-size router (router_mfma.hip): approximate logits on MFMA into approx [T][E+1] and
 // squared router-row norms into nw2 [E], then per token a certified top-k whose ids, order and
 // weights equal those of the canonical logits (weights[T*top_k + t] = shared gate when

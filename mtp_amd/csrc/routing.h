@@ -283,7 +283,7 @@ MOE_DEV float topk_weight(float my_v, int top_k, int lane) {
 template <int MAXC>
 MOE_DEV void topk_token(const float* __restrict__ row, int E, int top_k, int has_shared, int T,
                         int t, int lane, int32_t* __restrict__ ids, float* __restrict__ weights,
-                        int* ids_lds) {
+                        int* ids_lds, int32_t* ids_mirror = nullptr) {
   // row[E] when has_shared, else zero; issued with the selection's loads
   const float g = __uint_as_float(
       buf_ld32(buf_rsrc(row, (uint32_t)(E + (has_shared ? 1 : 0)) * 4u), (uint32_t)E * 4u));
@@ -295,6 +295,7 @@ MOE_DEV void topk_token(const float* __restrict__ row, int E, int top_k, int has
     ids[(int64_t)t * top_k + lane] = my_i;
     weights[(int64_t)t * top_k + lane] = w;
     if (ids_lds) ids_lds[t * top_k + lane] = my_i;
+    if (ids_mirror) ids_mirror[(int64_t)t * top_k + lane] = my_i;
   }
   if (has_shared && lane == 0) weights[(int64_t)T * top_k + t] = 1.0f / (1.0f + expf(-g));
 }
@@ -317,11 +318,12 @@ MOE_DEV void topk_token_lds(const float* __restrict__ row, int E, int top_k, int
 // topk_token / topk_token_lds for any E <= 512 (a uniform branch on E).
 MOE_DEV void topk_token_any(const float* __restrict__ row, int E, int top_k, int has_shared, int T,
                             int t, int lane, int32_t* __restrict__ ids,
-                            float* __restrict__ weights, int* ids_lds) {
+                            float* __restrict__ weights, int* ids_lds,
+                            int32_t* ids_mirror = nullptr) {
   if (E <= 256)
-    topk_token<4>(row, E, top_k, has_shared, T, t, lane, ids, weights, ids_lds);
+    topk_token<4>(row, E, top_k, has_shared, T, t, lane, ids, weights, ids_lds, ids_mirror);
   else
-    topk_token<8>(row, E, top_k, has_shared, T, t, lane, ids, weights, ids_lds);
+    topk_token<8>(row, E, top_k, has_shared, T, t, lane, ids, weights, ids_lds, ids_mirror);
 }
 MOE_DEV void topk_token_lds_any(const float* __restrict__ row, int E, int top_k, int lane,
                                 int* ids_lds, float* w_lds) {

@@ -380,6 +380,9 @@ class OffloadDecoder:
         self._pred_host: torch.Tensor | None = None
         self._ws: torch.Tensor | None = None
         self._pred_ws: torch.Tensor | None = None
+        self._lib = _lib.load()
+        self._prepared: tuple | None = None
+        self._layer_args: list[tuple] = []
 
     def predict(self, h: torch.Tensor) -> list[list[int]]:
         """Per layer, the distinct experts of the predictor's top-prefetch_k over h's rows.
@@ -411,27 +414,61 @@ class OffloadDecoder:
         torch.cuda.current_stream().synchronize()
         return [list(dict.fromkeys(self._pred_host[l].reshape(-1).tolist())) for l in range(L)]
 
+    def _prepare(self, x: torch.Tensor) -> None:
+        """Checks of every layer's router and bias, the workspace, the pinned ids buffer and the
+        per-layer call arguments, once per (batch size, device): a step's layer calls then run
+        no Python checks (routed_layer's, done here for all layers at once)."""
+        key = (x.shape[0], x.device)
+        if self._prepared == key:
+            return
+        T, pool = x.shape[0], self.pool
+        ex0 = pool.layer_experts(0)
+        for l in range(pool.num_layers):
+            ops._bf16_matrix(self.routers[l], "router_w", ex0.hidden_size)
+            if self.routers[l].shape[0] != ex0.num_experts:
+                raise ValueError(f"router_w of layer {l} has {self.routers[l].shape[0]} rows for "
+                                 f"{ex0.num_experts} experts")
+            ops._require_gpu(x, self.routers[l], self.biases[l])
+        p = ops._path(self.path)
+        need = ops.workspace_bytes(T, self.top_k, ex0, False, p)
+        if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
+            self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        self._ids_host = torch.empty((T, self.top_k), dtype=torch.int32, pin_memory=True)
+        structs = [pool.layer_experts(l).struct() for l in range(pool.num_layers)]
+        self._layer_args = [(self.routers[l].data_ptr(), ops._ptr(self.biases[l]), ctypes.byref(st),
+                             st) for l, st in enumerate(structs)]
+        self._path_id = p
+        self._prepared = key
+
     def step(self, x: torch.Tensor, prefetch: list[list[int]] | None = None,
              trace: list | None = None) -> list[torch.Tensor]:
         """One decode step over every layer; `prefetch[l]` is issued right after layer l.
+        Returns the layers' outputs (bf16 [T, H] each, views of one [L, T, H] tensor).
 
         trace: if given, one (layer, demanded experts, prefetched experts, host time in us)
         record per layer call is appended (the call's demand and prefetch happen inside it, after
         the routed ids reached the host), so the sequence can be replayed through the
         reference's virtual-time managers (mtp_amd.cache_manager)."""
+        L, H = self.pool.num_layers, self.pool.hidden
+        ops._bf16_matrix(x, "input", H)
+        ops._require_gpu(x)
+        if prefetch is not None and len(prefetch) < L:
+            raise ValueError(f"prefetch lists for {len(prefetch)} of {L} layers")
+        self._prepare(x)
         T = x.shape[0]
-        need = ops.workspace_bytes(T, self.top_k, self.pool.layer_experts(0), False, self.path)
-        if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=x.device)
-        outs = []
-        for l in range(self.pool.num_layers):
-            out, self._ids_host = routed_layer(x, self.routers[l], self.pool, l, top_k=self.top_k,
-                                               logit_bias=self.biases[l], ids_host=self._ids_host,
-                                               path=self.path, workspace=self._ws,
-                                               prefetch=prefetch[l] if prefetch is not None else None)
-            outs.append(out)
+        out = torch.empty((L, T, H), dtype=torch.bfloat16, device=x.device)
+        fn, check = self._lib.moe_offload_layer_v1, _lib.check
+        handle, stream = self.pool.cache.handle, ops._stream()
+        xp, op, row = x.data_ptr(), out.data_ptr(), T * H * 2
+        wsp, wsn, ids = self._ws.data_ptr(), self._ws.numel(), self._ids_host.data_ptr()
+        top_k, path = self.top_k, self._path_id
+        for l, (rp, bp, sp, _) in enumerate(self._layer_args):
+            pre = prefetch[l] if prefetch is not None else ()
+            n = len(pre)
+            arr = (ctypes.c_int32 * max(n, 1))(*map(int, pre))
+            check(fn(handle, l, xp, T, rp, bp, top_k, sp, wsp, wsn, op + l * row, ids, arr, n,
+                     path, stream, None))
             if trace is not None:
-                trace.append((l, self._ids_host.reshape(-1).tolist(),
-                              list(prefetch[l]) if prefetch is not None else [],
+                trace.append((l, self._ids_host.reshape(-1).tolist(), list(pre),
                               time.perf_counter() * 1e6))
-        return outs
+        return list(out.unbind(0))

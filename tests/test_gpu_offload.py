@@ -122,6 +122,32 @@ def test_offload_layer_call_matches_resident_layer(pooled, T, path):
     _slot_bytes_ok(pool, layer, resident, pack_blobs(g.experts))
 
 
+@pytest.mark.parametrize("where", ["pageable", "pinned_at_an_offset"])
+def test_offload_layer_ids_reach_any_host_buffer(pooled, where):
+    """The routed ids reach pageable host memory (a copy on the stream) and pinned memory at an
+    offset into its allocation (written by the top-k kernel through the mapping) alike."""
+    _say(f"offload layer ids into {where} memory")
+    layers, pool = pooled
+    layer, T = 0, 3
+    g = layers[layer]
+    x = synth.make_tokens(T, 512, seed=123).cuda()
+    if where == "pageable":
+        ids_buf = torch.full((T, 4), -7, dtype=torch.int32)
+    else:
+        big = torch.full((T * 4 + 40,), -7, dtype=torch.int32, pin_memory=True)
+        ids_buf = big[13:13 + T * 4].view(T, 4)
+    out, ids_host = routed_layer(x, g.router_w, pool, layer, top_k=4, logit_bias=g.logit_bias,
+                                 ids_host=ids_buf, path="decode")
+    want, ids, _ = ops.moe_layer(x, g.router_w, g.experts, top_k=4, logit_bias=g.logit_bias,
+                                 path="decode", return_routing=True)
+    torch.cuda.synchronize()
+    assert ids_host.data_ptr() == ids_buf.data_ptr()
+    assert np.array_equal(ids_host.numpy(), ids.cpu().numpy())
+    assert torch.equal(out, want)
+    if where != "pageable":
+        assert bool((big[:13] == -7).all()) and bool((big[13 + T * 4:] == -7).all())
+
+
 @pytest.mark.parametrize("T,L,H,D,E,k", [(1, 3, 512, 256, 64, 16), (4, 2, 2048, 1024, 256, 16),
                                           (3, 1, 256, 64, 40, 5)])
 def test_predictor_matches_oracle(T, L, H, D, E, k):
