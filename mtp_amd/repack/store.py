@@ -6,7 +6,8 @@ Format (src/mtp_expert_prefetch/repack/qwen3_moe_gptq.py:142-198 and store.py:39
                               "tensors": {key: {"shape", "dtype", "sha256"}}}
   <dir>/layer_XX.safetensors  keys "experts.{proj}.{kind}" stacked over experts.
 Same public names and errors as the reference's RepackedMoeExpertStore, plus
-``load_layer`` which returns a whole layer as a device-resident MoeExperts.
+``load_layer`` which returns a whole layer as a device-resident MoeExperts. Stores are written
+from a checkpoint snapshot by mtp_amd.repack.qwen3_moe_gptq.repack_qwen3_moe_gptq.
 """
 
 from __future__ import annotations
@@ -252,7 +253,8 @@ class RepackedMoeExpertStore:
 
 def write_repacked_store(out_dir: str | Path, layers: dict[int, dict[str, torch.Tensor]],
                          *, num_experts: int) -> Path:
-    """Write layers ({key: stacked tensor}) in the repacked format (for fixtures and tests)."""
+    """Write already stacked layers ({key: stacked tensor}) in the repacked format (fixtures and
+    tests; a checkpoint snapshot goes through qwen3_moe_gptq.repack_qwen3_moe_gptq)."""
     from safetensors.torch import save_file
 
     out = Path(out_dir)
