@@ -68,18 +68,35 @@ def parse_args() -> argparse.Namespace:
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_decode_w1_bs64_hbm_traffic.md"
+# the sources of the W1 decode kernel whose digest the traffic summary records
+TRAFFIC_SOURCES = ("mtp_amd/csrc/gemm_decode.hip", "mtp_amd/csrc/common.h")
 
 
-def profiled_traffic(batch: int) -> float | None:
+def kernel_source_digest() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
+
+
+def profiled_traffic(batch: int) -> tuple[float | None, str | None]:
     """HBM bytes per W1 decode launch at batch 64 from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE scaled by a known-size streaming kernel); None when the run
-    measures another kernel or batch, or the summary is absent."""
-    if batch != 64 or not TRAFFIC_PROFILE.exists():
-        return None
+    (FETCH_SIZE and WRITE_SIZE scaled by a known-size streaming kernel), and why it is absent:
+    None when the run measures another batch, the summary is missing, or the summary was
+    collected on other kernel sources (its source digest differs from this tree's)."""
+    if batch != 64:
+        return None, "the summary covers batch 64"
+    if not TRAFFIC_PROFILE.exists():
+        return None, "no traffic summary"
+    fields = {}
     for line in TRAFFIC_PROFILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        for key in ("traffic_bytes_per_launch:", "kernel_sources_sha256:"):
+            if line.startswith(key):
+                fields[key] = line.split(":", 1)[1].strip()
+    if fields.get("kernel_sources_sha256:") != kernel_source_digest():
+        return None, "the summary was collected on other kernel sources"
+    return float(fields["traffic_bytes_per_launch:"]), None
 
 
 def median_event_ms(fn, steps: int, stream) -> list[float]:
@@ -238,7 +255,7 @@ def main() -> int:
     w1_ms = statistics.median(median_event_ms(gw1.replay, args.steps, stream))
     w1_launch_us = w1_ms * 1e3 / L
     w1_bytes_per_launch = sum(r[3] for r in routed) * w1_per_expert / L
-    traffic = profiled_traffic(Tr)
+    traffic, traffic_note = profiled_traffic(Tr)
     roofline = {
         "bound": "hbm",
         "kernel": f"gemm_decode_kernel<W1> (gate_up + SiLU*mul), bs={Tr}",
@@ -246,7 +263,8 @@ def main() -> int:
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "traffic": traffic,
-        "traffic_source": TRAFFIC_PROFILE.name if traffic else None,
+        "traffic_source": (f"{TRAFFIC_PROFILE.name} (kernel sources sha256 "
+                           f"{kernel_source_digest()[:12]})") if traffic else traffic_note,
         "launch_us": w1_launch_us,
         "algorithmic_bytes_per_launch": w1_bytes_per_launch,
     }
