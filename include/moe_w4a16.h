@@ -380,8 +380,9 @@ int moe_slot_cache_stats_v1(uint64_t handle, moe_slot_cache_counters_v1* out);
 int moe_slot_cache_slot_of_v1(uint64_t handle, int32_t layer, int32_t expert);
 
 /* One offloaded MoE layer of a decode step in one call: router logits and top-k into the
- * workspace, the routed ids to ids_host (pinned host, T * top_k; the call waits for them on
- * stream), moe_slot_cache_demand_v1, the routed experts from the layer's slots (experts = the
+ * workspace, the routed ids to ids_host (host, T * top_k int32; the call waits for them on
+ * stream: memory from hipHostMalloc receives them from the top-k kernel itself, other host
+ * memory through a copy), moe_slot_cache_demand_v1, the routed experts from the layer's slots (experts = the
  * layer's slot view, as for moe_fused_experts_v1), when n_prefetch > 0 the prefetch of the host
  * list prefetch (as moe_slot_cache_prefetch_v1, with the demand's slots still pinned and without
  * the copy streams' wait for the compute stream, which the ids' wait has already drained), then

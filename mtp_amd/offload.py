@@ -322,11 +322,14 @@ def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts
                  workspace: torch.Tensor | None = None,
                  prefetch: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """One offloaded MoE layer in one native call (moe_offload_layer_v1): router -> ids to the
-    host -> demand -> experts from the slots -> layer_done [-> prefetch of `prefetch`].
+    host -> demand -> experts from the slots [-> prefetch of `prefetch`, the demand's slots still
+    pinned] -> layer_done.
 
     The host wait for the routed ids is the one synchronisation per layer that a host-managed
     cache needs (the reference's demand() is a host call on the routed ids too,
-    cache_manager.py:233-247). Returns (out bf16 [T, H], routed ids on the host int32 [T, k]).
+    cache_manager.py:233-247). A pinned ids_host (the default) receives the ids from the top-k
+    kernel itself; a pageable one gets a copy. Returns (out bf16 [T, H], routed ids on the host
+    int32 [T, k]).
     """
     lib = _lib.load()
     ex = pool.layer_experts(layer)
@@ -355,9 +358,10 @@ def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts
 class OffloadDecoder:
     """Decode steps through offloaded MoE layers, with prefetch of predicted experts.
 
-    Per layer: router -> routed ids to the host -> demand (misses copied on the compute stream)
-    -> experts from the layer's slots -> prefetch of the experts predicted for the next step
-    (side stream, ordered after this layer's kernels so a slot is never overwritten while read).
+    Per layer, one moe_offload_layer_v1 call: router -> routed ids to the host -> demand (misses
+    copied on the compute stream) -> experts from the layer's slots -> prefetch of the experts
+    predicted for the next step on the copy streams (the demand's slots stay pinned, so no slot
+    the layer's kernels read is overwritten) -> layer_done.
     Each layer reads the step's hidden state x (independent synthetic layers).
     """
 

@@ -451,7 +451,8 @@ def test_offload_decoder_at_the_full_config5_shape():
     prefetch lists (the hidden-residual predictor) after every layer. Every step's per-layer
     output equals the resident layer's bit for bit, and the slot cache's counters equal one
     LRU oracle per layer (cache_manager.py:208-279) fed the same demanded ids and prefetch lists
-    (prefetches follow layer_done, so no slot is pinned when they run)."""
+    (the demand's slots, still pinned while the layer call prefetches, are the layer's most
+    recently used, so with 64 slots the LRU victim is never one of them)."""
     from mtp_amd.offload import OffloadDecoder
     from mtp_amd.predictor import HiddenResidualExpertPredictor
     from oracle.cache_ref import LruCounters
