@@ -1,6 +1,8 @@
 // extern "C" entry points of libmoe_w4a16.so: argument validation, workspace carving and
 // stream-ordered orchestration of the kernels. No entry point allocates device memory or
 // synchronises the host.
+#include <atomic>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -645,6 +647,35 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
   return run_experts(x, T, top_k, experts, shared, L, workspace, out, path, routing, s);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Spins until flags[t] == seq for every t < T (the top-k kernel's system-scope releases after
+// the ids), for at most kFlagSpinUs; false on time-out (the caller then waits on the stream,
+// which also reports a failed kernel).
+constexpr double kFlagSpinUs = 200000.0;
+bool wait_flags(const int32_t* flags, int T, int32_t seq) {
+  const volatile int32_t* f = flags;
+  const auto t0 = std::chrono::steady_clock::now();
+  for (uint64_t it = 0;; ++it) {
+    int t = 0;
+    while (t < T && f[t] == seq) ++t;
+    if (t == T) {
+      std::atomic_thread_fence(std::memory_order_acquire);  // the ids after their flags
+      return true;
+    }
+    if ((it & 1023) == 1023 &&
+        std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count() >
+            kFlagSpinUs)
+      return false;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
 int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32_t T,
                          const uint16_t* router_w, const float* logit_bias, int32_t top_k,
                          const moe_expert_set_v1* experts, void* workspace,
@@ -691,12 +722,22 @@ int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32
     else
       (void)hipGetLastError();  // a failed lookup must not surface at the next launch check
   }
-  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, 0, ids, w, s, mirror),
+  // With mapped ids, the top-k kernel also raises one flag per token in the cache's mapped
+  // signal words after the token's ids: the host spins on them instead of waiting for the
+  // stream (whose completion signal arrives about 5 us later). The kernels enqueued before the
+  // top-k have completed when it runs, so the layer's slots are as free as after a stream wait.
+  int32_t seq = 0;
+  int32_t* flags = mirror ? slot_cache_signal(cache, T, &seq) : nullptr;
+  MOE_CHECK_HIP(launch_router_topk(logits, T, E, top_k, 0, ids, w, s, mirror, flags, seq),
                 "offload layer: router topk");
   if (!mirror)
     MOE_CHECK_HIP(hipMemcpyAsync(ids_host, ids, (size_t)n * 4, hipMemcpyDeviceToHost, s),
                   "offload layer: ids to the host");
-  MOE_CHECK_HIP(hipStreamSynchronize(s), "offload layer: wait for the ids");
+  if (!flags || !wait_flags(flags, T, seq)) {
+    MOE_CHECK_HIP(hipStreamSynchronize(s), "offload layer: wait for the ids");
+    if (flags && !wait_flags(flags, T, seq))
+      return fail(MOE_ERR_UNSUPPORTED, "offload layer: the routed ids' flags were not raised");
+  }
   rc = moe_slot_cache_demand_v1(cache, layer, ids_host, n, stream, hits);
   if (rc) return rc;
   const Routing routing =

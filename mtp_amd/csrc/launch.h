@@ -15,6 +15,10 @@ char* moe_error_buffer();
 // the layer was enqueued, and the latest demand's slots are still pinned.
 int slot_cache_prefetch_synced(uint64_t handle, int32_t layer, const int32_t* experts, int32_t n,
                                void* compute_stream);
+// The slot cache's routed-ids flags for an offload layer call of T tokens (slot_cache.hip):
+// pinned host words mapped at the same device address, and the value this call waits for;
+// nullptr when unavailable (then the call waits on its stream).
+int32_t* slot_cache_signal(uint64_t handle, int32_t T, int32_t* seq);
 
 // Argument checks of a routed layer call that involve no workspace (api.hip): 0 or the error
 // code moe_layer_v1 returns for the same input (message in moe_error_buffer).
@@ -34,9 +38,12 @@ hipError_t launch_router_logits(const uint16_t* x, int T, int H, const uint16_t*
                                 hipStream_t stream);
 // ids_mirror: optional second destination of the ids (e.g. pinned host memory mapped into the
 // device's address space), written by the same lanes as ids.
+// flags (with ids_mirror): after token t's ids are out, word t is set to seq with a
+// system-scope release, so a host that reads flags[t] == seq then reads the token's ids.
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
                               int32_t* ids, float* weights, hipStream_t stream,
-                              int32_t* ids_mirror = nullptr);
+                              int32_t* ids_mirror = nullptr, int32_t* flags = nullptr,
+                              int32_t seq = 0);
 // Prefill-size router (router_mfma.hip): approximate logits on MFMA into approx [T][E+1] and
 // squared router-row norms into nw2 [E], then per token a certified top-k whose ids, order and
 // weights equal those of the canonical logits (weights[T*top_k + t] = shared gate when

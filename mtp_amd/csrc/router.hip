@@ -244,12 +244,18 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
                                                           int E, int top_k, int has_shared,
                                                           int32_t* __restrict__ ids,
                                                           float* __restrict__ weights,
-                                                          int32_t* __restrict__ ids_mirror) {
+                                                          int32_t* __restrict__ ids_mirror,
+                                                          int32_t* __restrict__ flags,
+                                                          int32_t seq) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= T) return;
   topk_token_any(logits + (int64_t)t * (E + 1), E, top_k, has_shared, T, t, lane, ids, weights,
                  nullptr, ids_mirror);
+  if (flags) {  // the token's ids (in host memory) before its flag
+    __threadfence_system();
+    if (lane == 0) __hip_atomic_store(flags + t, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // One wave per token for the top-k, then wave 0 aligns the (at most 64) slots.
@@ -323,11 +329,11 @@ hipError_t launch_router_logits_norm(const uint16_t* res_in, const uint16_t* add
 
 hipError_t launch_router_topk(const float* logits, int T, int E, int top_k, int has_shared,
                               int32_t* ids, float* weights, hipStream_t stream,
-                              int32_t* ids_mirror) {
+                              int32_t* ids_mirror, int32_t* flags, int32_t seq) {
   const int blocks = (T + 3) / 4;
   if (blocks == 0) return hipSuccess;
   hipLaunchKernelGGL(router_topk_kernel, dim3(blocks), dim3(256), 0, stream, logits, T, E, top_k,
-                     has_shared, ids, weights, ids_mirror);
+                     has_shared, ids, weights, ids_mirror, flags, seq);
   return hipGetLastError();
 }
 

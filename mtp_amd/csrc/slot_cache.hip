@@ -48,6 +48,7 @@ namespace {
 constexpr uint64_t kMagic = 0x4D4F45534C4F5431ull;  // "MOESLOT1"
 constexpr int kStagingRing = 512;
 constexpr int kEventRing = 1024;  // timing events of prefetch calls and of demands
+constexpr int kSignalWords = 64;  // routed-ids flags: one per token of an offload layer call
 // Copy streams of the prefetches: one DMA stream moves about 42 GB/s of expert blobs from
 // pinned host memory, two together about 53 GB/s, four no more (MI355X, measured); a slot's
 // copies always use the same stream (slot index modulo the count). (Splitting a demand's misses over the compute stream and a second stream measured
@@ -91,6 +92,11 @@ struct Cache {
   hipStream_t side[kCopyStreams] = {};  // prefetch copies
   hipEvent_t compute_mark = nullptr;
   int32_t* staging = nullptr;  // pinned [kStagingRing][num_experts]
+  // pinned [kSignalWords], mapped at the same address on the device (nullptr if HIP maps it
+  // elsewhere): the routed-ids flags of moe_offload_layer_v1, one per token; signal_seq is the
+  // value the latest call waits for
+  int32_t* signal = nullptr;
+  uint32_t signal_seq = 0;
   std::vector<hipEvent_t> staging_done;
   int staging_next = 0;
   // timing events: pf_ev[(seq % kEventRing) * kCopyStreams + stream], dm_ev[seq % kEventRing]
@@ -220,6 +226,18 @@ int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handl
     SC_HIP(hipEventCreateWithFlags(&c->compute_mark, hipEventDisableTiming), "create event");
     SC_HIP(hipHostMalloc((void**)&c->staging, (size_t)kStagingRing * d.num_experts * 4,
                          hipHostMallocDefault), "pinned staging");
+    {
+      void* sig = nullptr;
+      void* dev = nullptr;
+      SC_HIP(hipHostMalloc(&sig, kSignalWords * 4, hipHostMallocDefault), "pinned signal words");
+      memset(sig, 0, kSignalWords * 4);
+      if (hipHostGetDevicePointer(&dev, sig, 0) == hipSuccess && dev == sig) {
+        c->signal = static_cast<int32_t*>(sig);
+      } else {
+        (void)hipGetLastError();
+        hipHostFree(sig);
+      }
+    }
     c->staging_done.assign(kStagingRing, nullptr);
     for (hipEvent_t& e : c->staging_done)
       SC_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "create event");
@@ -244,6 +262,7 @@ int moe_slot_cache_destroy_v1(uint64_t handle) {
     hipEventDestroy(c->compute_mark);
     for (hipStream_t st : c->side) hipStreamDestroy(st);
     hipHostFree(c->staging);
+    if (c->signal) hipHostFree(c->signal);
   }
   c->magic = 0;
   delete c;
@@ -321,6 +340,17 @@ int prefetch_impl(Cache* c, int32_t layer, const int32_t* experts, int32_t n,
 }
 
 }  // namespace
+
+// The routed-ids flags of the next offload layer call: the mapped words (nullptr when the cache
+// has none, or T exceeds them) and the value the call's top-k kernel will write into words
+// [0, T) once the ids are out; never 0, so words from earlier calls or from creation differ.
+int32_t* slot_cache_signal(uint64_t handle, int32_t T, int32_t* seq) {
+  Cache* c = from_handle(handle);
+  if (!c || !c->signal || T < 1 || T > kSignalWords) return nullptr;
+  if (++c->signal_seq == 0) c->signal_seq = 1;
+  *seq = (int32_t)c->signal_seq;
+  return c->signal;
+}
 
 // Prefetch for a caller that synchronised the compute stream after enqueueing every kernel
 // that reads the layer's slots, except the kernels of the layer's latest demand, whose slots
