@@ -645,7 +645,7 @@ def offload_bench(layers, pool, args, dev) -> dict:
             "counters": diff,
             "last_step_equals_resident_layers": bool(spot),
             "reference_semantics": ready_time_replay(trace, L * args.offload_slots,
-                                                     calib["eight_experts_us_per_expert"]["p50"],
+                                                     calib["two_streams_us_per_expert"]["p50"],
                                                      args.offload_warmup * L),
         }
         rs = runs[name]["reference_semantics"]
@@ -672,7 +672,8 @@ def ready_time_replay(trace, capacity: int, service_us: float, skip: int) -> dic
     """The offload run's call sequence (per layer call: demanded ids, then the prefetch list, at
     the host time the call made them) through the reference's ReadyTimeExpertCacheManager
     (cache_manager.py:298-578, native): one LRU of `capacity` keys, each issue a transfer of
-    `service_us` (the measured pinned H2D time per expert), batches of one, no deadline. A
+    `service_us` (the measured pinned H2D time per expert when copies alternate over two
+    streams, as the slot cache's prefetches do), batches of one, no deadline. A
     demand then hits only experts whose virtual transfer completed by its arrival; a demand of
     one still in flight is a ready-late miss. Counters cover the calls after the first `skip`
     (the warmup steps), as the measured counters do."""
@@ -701,7 +702,8 @@ def ready_time_replay(trace, capacity: int, service_us: float, skip: int) -> dic
 def h2d_calibration(pool, reps: int = 200) -> dict:
     """Pinned host -> HBM copy of expert blobs with hipMemcpyAsync (the slot cache's copy), timed
     with HIP events on one stream: single blobs and batches of 8, p50 / p95, beside the reference's
-    measured copy (W7900, PCIe 4.0 x16)."""
+    measured copy (W7900, PCIe 4.0 x16); then batches of 16 split over two streams, as the slot
+    cache's two copy streams move prefetches (the per-expert service time of its transfers)."""
     import ctypes
 
     import torch
@@ -733,10 +735,34 @@ def h2d_calibration(pool, reps: int = 200) -> dict:
         b.synchronize()
         return a.elapsed_time(b) * 1e3  # us
 
+    side = [torch.cuda.Stream(), torch.cuda.Stream()]
+
+    def timed_two(n: int, rep: int) -> float:  # n blobs alternating over the two side streams
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for st in side:
+            st.wait_stream(stream)
+        for j in range(n):
+            i = rep * n + j
+            src = pool.host.ptr + (i * 7919 % n_blobs) * blob
+            err = hip.hipMemcpyAsync(ctypes.c_void_p(dst.data_ptr() + (i % n_dst) * blob),
+                                     ctypes.c_void_p(src), blob, 1,
+                                     ctypes.c_void_p(side[j % 2].cuda_stream))
+            if err != 0:
+                raise RuntimeError(f"hipMemcpyAsync failed with HIP error {err}")
+        for st in side:
+            stream.wait_stream(st)
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) * 1e3  # us
+
     for r in range(10):
         timed(8, r)
+        timed_two(16, r)
     one = [timed(1, r) for r in range(reps)]
     eight = [timed(8, r) for r in range(reps // 2)]
+    two = [timed_two(16, r) for r in range(reps // 2)]
     out = {
         "expert_bytes": blob,
         "one_expert_us": {"p50": statistics.median(one), "p95": pct(one, 0.95)},
@@ -745,7 +771,10 @@ def h2d_calibration(pool, reps: int = 200) -> dict:
         "eight_experts_us_per_expert": {"p50": statistics.median(eight) / 8,
                                         "p95": pct(eight, 0.95) / 8},
         "eight_experts_GBps_p50": 8 * blob / statistics.median(eight) / 1e3,
-        "samples": {"one": len(one), "eight": len(eight)},
+        "two_streams_us_per_expert": {"p50": statistics.median(two) / 16,
+                                      "p95": pct(two, 0.95) / 16},
+        "two_streams_GBps_p50": 16 * blob / statistics.median(two) / 1e3,
+        "samples": {"one": len(one), "eight": len(eight), "two_streams": len(two)},
         "reference_w7900_pcie4": {"one_expert_GBps_p95": 20.43, "eight_experts_GBps_p50": 28.23,
                                   "eight_experts_us_per_expert_p95": 62.09,
                                   "expert_bytes": 1.65e6,
@@ -754,7 +783,8 @@ def h2d_calibration(pool, reps: int = 200) -> dict:
     log(f"[bench] H2D calibration: 1 expert ({blob / 1e6:.2f} MB) p50 {out['one_expert_us']['p50']:.1f} us "
         f"p95 {out['one_expert_us']['p95']:.1f} us ({out['one_expert_GBps_p95']:.1f} GB/s at p95); "
         f"8 experts {out['eight_experts_GBps_p50']:.1f} GB/s at p50, "
-        f"{out['eight_experts_us_per_expert']['p95']:.1f} us per expert at p95")
+        f"{out['eight_experts_us_per_expert']['p95']:.1f} us per expert at p95; 16 experts over two "
+        f"streams {out['two_streams_GBps_p50']:.1f} GB/s at p50")
     return out
 
 
