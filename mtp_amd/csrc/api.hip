@@ -1,6 +1,6 @@
 // extern "C" entry points of libmoe_w4a16.so: argument validation, workspace carving and
-// stream-ordered orchestration of the kernels. No entry point allocates device memory or
-// synchronises the host.
+// stream-ordered orchestration of the kernels. No entry point allocates device memory; none
+// synchronises the host except the offload layer call, which waits for its routed ids.
 #include <atomic>
 #include <chrono>
 #include <cstdarg>

@@ -51,8 +51,9 @@ constexpr int kEventRing = 1024;  // timing events of prefetch calls and of dema
 constexpr int kSignalWords = 64;  // routed-ids flags: one per token of an offload layer call
 // Copy streams of the prefetches: one DMA stream moves about 42 GB/s of expert blobs from
 // pinned host memory, two together about 53 GB/s, four no more (MI355X, measured); a slot's
-// copies always use the same stream (slot index modulo the count). (Splitting a demand's misses over the compute stream and a second stream measured
-// slower: the cross-stream wait costs more than the parallel copy saves.)
+// copies always use the same stream (slot index modulo the count). (Splitting a demand's
+// misses over the compute stream and a second stream measured slower: the cross-stream wait
+// costs more than the parallel copy saves.)
 constexpr int kCopyStreams = 2;
 
 struct Slot {
