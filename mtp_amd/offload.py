@@ -420,9 +420,11 @@ class OffloadDecoder:
 
     def _prepare(self, x: torch.Tensor) -> None:
         """Checks of every layer's router and bias, the workspace, the pinned ids buffer and the
-        per-layer call arguments, once per (batch size, device): a step's layer calls then run
-        no Python checks (routed_layer's, done here for all layers at once)."""
-        key = (x.shape[0], x.device)
+        per-layer call arguments, once per (batch size, device, top_k, path, router and bias
+        tensors): a step's layer calls then run no Python checks (routed_layer's, done here for
+        all layers at once). A router or bias replaced between steps is checked again."""
+        key = (x.shape[0], x.device, self.top_k, self.path,
+               tuple(r.data_ptr() for r in self.routers), tuple(map(ops._ptr, self.biases)))
         if self._prepared == key:
             return
         T, pool = x.shape[0], self.pool

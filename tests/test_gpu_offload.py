@@ -506,3 +506,40 @@ def test_offload_decoder_at_the_full_config5_shape():
              f"{st['issued_fetch_count']}")
     finally:
         pool.close()
+
+
+def test_offload_decoder_rechecks_replaced_routers_and_top_k():
+    """OffloadDecoder caches each layer's call arguments between steps; a router or bias tensor
+    replaced in `routers`/`biases`, or a new top_k, must be picked up by the next step (outputs
+    equal the resident layers with the new arguments)."""
+    from mtp_amd.offload import OffloadDecoder
+    _say("offload decoder: replaced router, bias and top_k between steps")
+    layers = [to_gpu(small_layer(l, zipf=True)) for l in range(2)]
+    pool = OffloadedExperts(2, 16, 512, 256, 16, group_size=128, device="cuda")
+    try:
+        for l, g in enumerate(layers):
+            pool.store_layer(l, g.experts)
+        torch.cuda.synchronize()
+        routers = [g.router_w for g in layers]
+        biases = [g.logit_bias for g in layers]
+        dec = OffloadDecoder(pool, routers, biases, top_k=4, path="decode")
+        x = torch.randn(2, 512, device="cuda").to(torch.bfloat16)
+
+        def check(top_k):
+            outs = dec.step(x)
+            for l, g in enumerate(layers):
+                want = ops.moe_layer(x, dec.routers[l], g.experts, top_k=top_k,
+                                     logit_bias=dec.biases[l], path="decode")
+                torch.cuda.synchronize()
+                assert torch.equal(outs[l], want), (l, top_k)
+
+        check(4)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(5)
+        dec.routers[1] = (torch.randn(16, 512, generator=gen, device="cuda") * 0.05).to(torch.bfloat16)
+        dec.biases[0] = None
+        check(4)
+        dec.top_k = 2
+        check(2)
+    finally:
+        pool.close()
