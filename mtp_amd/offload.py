@@ -337,6 +337,7 @@ def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts
     ops._bf16_matrix(router_w, "router_w", ex.hidden_size)
     if router_w.shape[0] != ex.num_experts:
         raise ValueError(f"router_w has {router_w.shape[0]} rows for {ex.num_experts} experts")
+    ops._check_bias_gate(logit_bias, None, ex.num_experts, ex.hidden_size)
     ops._require_gpu(x, router_w, logit_bias)
     T = x.shape[0]
     p = ops._path(path)
@@ -434,6 +435,7 @@ class OffloadDecoder:
             if self.routers[l].shape[0] != ex0.num_experts:
                 raise ValueError(f"router_w of layer {l} has {self.routers[l].shape[0]} rows for "
                                  f"{ex0.num_experts} experts")
+            ops._check_bias_gate(self.biases[l], None, ex0.num_experts, ex0.hidden_size)
             ops._require_gpu(x, self.routers[l], self.biases[l])
         p = ops._path(self.path)
         need = ops.workspace_bytes(T, self.top_k, ex0, False, p)

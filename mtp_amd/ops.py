@@ -69,6 +69,28 @@ def _bf16_matrix(x: torch.Tensor, name: str, cols: int | None = None) -> None:
         raise ValueError(f"Expected {name} last dim {cols}, got {x.shape[1]}")
 
 
+def _check_bias_gate(logit_bias: torch.Tensor | None, shared_gate_w: torch.Tensor | None,
+                     E: int, H: int) -> None:
+    """The kernels read E float32 biases and H bf16 shared-gate weights."""
+    if logit_bias is not None and (logit_bias.dtype != torch.float32 or logit_bias.numel() != E):
+        raise ValueError("logit_bias must be float32 [E]")
+    if shared_gate_w is not None and (shared_gate_w.dtype != torch.bfloat16
+                                      or shared_gate_w.numel() != H):
+        raise ValueError("shared_gate_w must be bfloat16 with hidden elements")
+
+
+def _check_blocks(sorted_ids: torch.Tensor, expert_ids: torch.Tensor, ntpp: torch.Tensor,
+                  block_m: int) -> None:
+    """align's outputs as the grouped GEMMs read them: expert_ids.numel() blocks of block_m
+    sorted slot ids and the padded total."""
+    for name, t in (("sorted_ids", sorted_ids), ("expert_ids", expert_ids), ("ntpp", ntpp)):
+        if t.dtype != torch.int32:
+            raise TypeError(f"{name} must be int32")
+    if sorted_ids.numel() < expert_ids.numel() * block_m or ntpp.numel() < 1:
+        raise ValueError(f"sorted_ids holds {sorted_ids.numel()} ids for {expert_ids.numel()} "
+                         f"blocks of {block_m}")
+
+
 # ----------------------------------------------------------------------------- dequant
 def dequantize(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
                g_idx: torch.Tensor | None = None, *, group_size: int = 128,
@@ -86,8 +108,24 @@ def dequantize(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor
     _require_gpu(qweight, qzeros, scales, g_idx)
     if dtype not in OUT_DTYPES:
         raise ValueError(f"Unsupported dtype {dtype}")
+    if qweight.ndim != 3 or qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+        raise TypeError("qweight [E, K/8, N] and qzeros must be int32")
+    if scales.dtype != torch.float16:
+        raise TypeError(f"scales must be float16, got {scales.dtype}")
     e, k8, n = qweight.shape
     k = k8 * 8
+    if group_size <= 0 or k % group_size != 0:
+        raise ValueError(f"group_size {group_size} does not divide in_features {k}")
+    ng = k // group_size
+    if tuple(scales.shape) != (e, ng, n) or tuple(qzeros.shape) != (e, ng, n // 8):
+        raise ValueError(f"scales {tuple(scales.shape)} / qzeros {tuple(qzeros.shape)} do not "
+                         f"match qweight {tuple(qweight.shape)} with group_size {group_size}")
+    if g_idx is not None:
+        if tuple(g_idx.shape) != (e, k):
+            raise ValueError(f"g_idx {tuple(g_idx.shape)} must be [E, K] = {(e, k)}")
+        lo, hi = (int(v) for v in torch.aminmax(g_idx))
+        if lo < 0 or hi >= ng:  # the kernel reads the scales and zeros row g_idx[k]
+            raise ValueError(f"g_idx out of range [{lo}, {hi}] for {ng} groups")
     out_shape = (e, n, k) if linear_weight else (e, k, n)
     out = torch.empty(out_shape, dtype=dtype, device=qweight.device)
     proj = _lib.GptqProj(qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr())
@@ -168,8 +206,12 @@ def w1_gateup_silu(x, experts: MoeExperts, sorted_ids, expert_ids, ntpp, *, top_
                    shared: MoeExperts | None = None, path: str | int = "auto") -> torch.Tensor:
     lib = _lib.load()
     p = _path(path)
+    _bf16_matrix(x, "input", experts.hidden_size)
+    _require_gpu(x, sorted_ids, expert_ids, ntpp)
+    _require_experts_on(x.device, experts, shared)
     T = x.shape[0]
     bm = _block_m(p, T, top_k)
+    _check_blocks(sorted_ids, expert_ids, ntpp, bm)
     slots = T * top_k + (T if shared is not None else 0)
     h = torch.empty(slots, experts.intermediate_size, dtype=torch.bfloat16, device=x.device)
     ex = experts.struct()
@@ -187,7 +229,16 @@ def w2_down(h, experts: MoeExperts, sorted_ids, expert_ids, ntpp, topk_weights_f
     """Weighted W2 rows ys fp32 [slots, H]; rows of dropped slots are left as they were."""
     lib = _lib.load()
     p = _path(path)
+    slots = T * top_k + (T if shared is not None else 0)
+    _bf16_matrix(h, "h", experts.intermediate_size)
+    if h.shape[0] < slots:
+        raise ValueError(f"h has {h.shape[0]} rows for {slots} slots")
+    if topk_weights_flat.dtype != torch.float32 or topk_weights_flat.numel() < slots:
+        raise ValueError(f"topk_weights_flat must be float32 with at least {slots} elements")
+    _require_gpu(h, sorted_ids, expert_ids, ntpp, topk_weights_flat)
+    _require_experts_on(h.device, experts, shared)
     bm = _block_m(p, T, top_k)
+    _check_blocks(sorted_ids, expert_ids, ntpp, bm)
     if ys is None:
         ys = torch.empty(h.shape[0], experts.hidden_size, dtype=torch.float32, device=h.device)
     elif (ys.dtype != torch.float32 or tuple(ys.shape) != (h.shape[0], experts.hidden_size)
@@ -272,6 +323,7 @@ def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, t
         raise ValueError(f"router_w has {router_w.shape[0]} rows for {experts.num_experts} experts")
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w must be given together")
+    _check_bias_gate(logit_bias, shared_gate_w, experts.num_experts, experts.hidden_size)
     _require_gpu(x, router_w, logit_bias, shared_gate_w)
     _require_experts_on(x.device, experts, shared)
     T = x.shape[0]
@@ -319,6 +371,7 @@ def norm_layer(res: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts,
         raise ValueError("norm_w must be a contiguous bfloat16 tensor of hidden elements")
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w must be given together")
+    _check_bias_gate(logit_bias, shared_gate_w, experts.num_experts, experts.hidden_size)
     _require_gpu(res, add, norm_w, router_w)
     if res_out is None:
         res_out = torch.empty_like(res)
@@ -356,6 +409,7 @@ def fused_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.T
         raise ValueError("topk_ids/topk_weights must be [T, k] matching the input rows")
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w must be given together")
+    _check_bias_gate(None, shared_gate_w, experts.num_experts, experts.hidden_size)
     _require_gpu(x, topk_ids, topk_weights, shared_gate_w)
     _require_experts_on(x.device, experts, shared)
     T, k = topk_ids.shape

@@ -161,3 +161,29 @@ def test_stepwise_entry_points_with_dropped_ids_and_poisoned_ys(path):
     err = moe_ref.rel_err(out.float().cpu().numpy(), ref)
     print(f"  {path}: rel_err={err:.3e}", flush=True)
     assert np.isfinite(err) and err <= LAYER_RTOL
+
+
+def test_wrappers_refuse_buffers_the_kernels_would_overrun():
+    """The tensor wrappers check what the C ABI cannot (it only sees pointers): shapes and
+    dtypes of the GPTQ tensors, g_idx's range, align's table sizes and the bias dtype."""
+    _say("wrapper argument checks")
+    from tests.helpers import small_layer, to_gpu
+    st = synth.make_projection(1, 256, 64, synth._gen(5, "cpu"), "cpu")
+    q, z, s = st.qweight.cuda(), st.qzeros.cuda(), st.scales.cuda()
+    with pytest.raises(ValueError, match="do not match"):
+        ops.dequantize(q, z, s[:, :1], group_size=128)
+    with pytest.raises(TypeError, match="float16"):
+        ops.dequantize(q, z, s.float(), group_size=128)
+    bad = torch.zeros(1, 256, dtype=torch.int32, device="cuda")
+    bad[0, 7] = 2
+    with pytest.raises(ValueError, match="out of range"):
+        ops.dequantize(q, z, s, bad, group_size=128)
+    g = to_gpu(small_layer(0))
+    x = torch.randn(4, 512, device="cuda").to(torch.bfloat16)
+    with pytest.raises(ValueError, match="logit_bias"):
+        ops.moe_layer(x, g.router_w, g.experts, top_k=4,
+                      logit_bias=torch.zeros(16, dtype=torch.bfloat16, device="cuda"))
+    ids, w, _, _ = ops.router_topk(x, g.router_w, 4)
+    sorted_ids, eids, ntpp = ops.align(ids, 16, 16)
+    with pytest.raises(ValueError, match="sorted_ids holds"):
+        ops.w1_gateup_silu(x, g.experts, sorted_ids[:16], eids, ntpp, top_k=4, path="decode")
