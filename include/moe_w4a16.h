@@ -129,7 +129,9 @@ int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_
  * every block (bf16 h [num_slots, I]). Replaces invoke_fused_moe_wna16_triton_kernel for
  * W1 + silu_and_mul (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19674-19718,
  * arithmetic at src/mtp_expert_prefetch/tracing/vllm_wna16_group_plan.py:367-486).
- * shared: NULL or the shared expert (expert id num_experts). */
+ * shared: NULL or the shared expert (expert id num_experts). sorted_ids, expert_ids and ntpp
+ * are moe_align_v1's outputs for the same block_m and capacity_blocks (the kernels read
+ * capacity_blocks * block_m sorted ids; the library cannot check the buffers' sizes). */
 int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
                           const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
                           const int32_t* sorted_ids, const int32_t* expert_ids,
@@ -138,7 +140,8 @@ int moe_w1_gateup_silu_v1(const uint16_t* x, int32_t T, int32_t top_k,
 
 /* W2: ys[f, :] = topk_weights[f] * (h[f] . Wdown[e]^T), fp32 [num_slots, H].
  * Replaces the W2 dispatch with mul_routed_weight=True, top_k=1
- * (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19761-19783). */
+ * (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19761-19783). Routing tables as for
+ * moe_w1_gateup_silu_v1; topk_weights fp32 [num_slots]. */
 int moe_w2_down_v1(const uint16_t* h, int32_t T, int32_t top_k,
                    const moe_expert_set_v1* experts, const moe_expert_set_v1* shared,
                    const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntpp,
