@@ -170,7 +170,9 @@ int moe_rmsnorm_v1(uint16_t* res, const uint16_t* add, int32_t T, int32_t hidden
                    const uint16_t* weight, float eps, uint16_t* out, void* stream);
 
 /* Workspace bytes for moe_layer_v1 / moe_fused_experts_v1 (no state survives between calls;
- * calls that share one workspace must be ordered on one stream). */
+ * calls that share one workspace must be ordered on one stream). Every workspace argument of
+ * this library must start on a 256-byte boundary (hipMalloc and torch allocations do); a
+ * misaligned one is refused with MOE_ERR_WORKSPACE. */
 int64_t moe_layer_workspace_bytes_v1(int32_t T, int32_t top_k, const moe_expert_set_v1* experts,
                                      int32_t has_shared, int32_t path);
 

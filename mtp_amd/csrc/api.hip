@@ -284,6 +284,8 @@ int moe_predictor_v1(const uint16_t* h, int32_t T, int32_t hidden, int32_t num_h
     return fail(MOE_ERR_SHAPE, "predictor: num_experts=%d top_k=%d", num_experts, top_k);
   if (workspace_bytes < moe_predictor_workspace_bytes_v1(T, num_heads, inner, num_experts, top_k))
     return fail(MOE_ERR_WORKSPACE, "predictor: workspace too small");
+  if (!workspace_aligned(workspace))
+    return fail(MOE_ERR_WORKSPACE, "predictor: workspace must be 256-byte aligned");
   const size_t L = num_heads;
   char* ws = static_cast<char*>(workspace);
   float* z1 = reinterpret_cast<float*>(ws);
@@ -508,6 +510,8 @@ int layer_impl(const uint16_t* x, int32_t T, const uint16_t* router_w, const flo
   if (workspace_bytes < (int64_t)L.total)
     return fail(MOE_ERR_WORKSPACE, "layer: workspace %lld < required %lld",
                 (long long)workspace_bytes, (long long)L.total);
+  if (!workspace_aligned(workspace))
+    return fail(MOE_ERR_WORKSPACE, "layer: workspace must be 256-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   float* logits = at<float>(workspace, L.logits);
   int32_t* ids = at<int32_t>(workspace, L.ids);
@@ -631,6 +635,8 @@ int moe_fused_experts_v1(const uint16_t* x, int32_t T, const int32_t* topk_ids,
   if (workspace_bytes < (int64_t)L.total)
     return fail(MOE_ERR_WORKSPACE, "experts: workspace %lld < required %lld",
                 (long long)workspace_bytes, (long long)L.total);
+  if (!workspace_aligned(workspace))
+    return fail(MOE_ERR_WORKSPACE, "experts: workspace must be 256-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   int32_t* ids = at<int32_t>(workspace, L.ids);
   float* w = at<float>(workspace, L.w);
@@ -698,6 +704,8 @@ int moe_offload_layer_v1(uint64_t cache, int32_t layer, const uint16_t* x, int32
   if (workspace_bytes < (int64_t)L.total)
     return fail(MOE_ERR_WORKSPACE, "offload layer: workspace %lld < required %lld",
                 (long long)workspace_bytes, (long long)L.total);
+  if (!workspace_aligned(workspace))
+    return fail(MOE_ERR_WORKSPACE, "offload layer: workspace must be 256-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   float* logits = at<float>(workspace, L.logits);
   int32_t* ids = at<int32_t>(workspace, L.ids);

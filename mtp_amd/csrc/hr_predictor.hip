@@ -212,6 +212,7 @@ int moe_hr_predictor_v1(const uint16_t* hidden, int32_t N, const int32_t* layer_
   if (workspace_bytes < hr_predictor_workspace(N, params->width, params->future_window,
                                                params->num_experts))
     return hr_fail(MOE_ERR_WORKSPACE, "workspace too small");
+  if (!workspace_aligned(workspace)) return hr_fail(MOE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   const hipError_t e = launch_hr_predictor(hidden, N, params->hidden, layer_ids, *params, prior,
                                            residual_scale, scale_per_example, top_k, workspace,
                                            logits_out, topk_ids, (hipStream_t)stream);

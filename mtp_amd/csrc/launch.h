@@ -10,6 +10,10 @@
 constexpr int kErrorBufferBytes = 512;
 char* moe_error_buffer();
 
+// Workspaces start on a 256-byte boundary (hipMalloc's and torch's allocations do): their
+// sections are laid out at 256-byte offsets and read with 16-byte vector and LDS-direct loads.
+inline bool workspace_aligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 255u) == 0; }
+
 // Slot-cache prefetch for moe_offload_layer_v1 (slot_cache.hip): no ordering wait on the compute
 // stream; the caller has synchronised that stream after every kernel reading an unpinned slot of
 // the layer was enqueued, and the latest demand's slots are still pinned.

@@ -256,6 +256,9 @@ int moe_slot_cache_destroy_v1(uint64_t handle) {
   if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
   if (live(c)) {
     hipSetDevice(c->d.device);
+    // Table uploads from the staging ring and the top-k kernel's flag stores into the signal
+    // words run on the caller's compute stream: wait for the whole device before freeing them.
+    hipDeviceSynchronize();
     for (hipStream_t st : c->side) hipStreamSynchronize(st);
     for (hipEvent_t e : c->staging_done) hipEventDestroy(e);
     for (hipEvent_t e : c->pf_ev) hipEventDestroy(e);

@@ -63,6 +63,21 @@ def test_workspace_too_small_is_rejected():
     assert rc == _lib.MOE_ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("base", [0x1004, 0x1080])
+def test_misaligned_workspace_is_rejected_before_any_launch(base):
+    """Workspaces start on 256-byte boundaries; an entry point refuses another base up front."""
+    lib = _lib.load()
+    ex = _fake_set()
+    need = lib.moe_layer_workspace_bytes_v1(16, 8, ctypes.byref(ex), 0, 0)
+    rc = lib.moe_layer_v1(0x10, 16, 0x10, None, 8, ctypes.byref(ex), None, None, base, need,
+                          0x10, None, None, 0, None)
+    assert rc == _lib.MOE_ERR_WORKSPACE
+    assert b"256-byte aligned" in lib.moe_w4a16_last_error()
+    rc = lib.moe_fused_experts_v1(0x10, 16, 0x10, 0x10, 8, ctypes.byref(ex), None, None, base,
+                                  need, 0x10, 0, None)
+    assert rc == _lib.MOE_ERR_WORKSPACE
+
+
 @pytest.mark.parametrize("path", [3, -1, 99])
 def test_unknown_path_is_refused(path):
     """Only AUTO, DECODE and PREFILL exist; any other path value is an error, never AUTO."""

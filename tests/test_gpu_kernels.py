@@ -187,3 +187,19 @@ def test_wrappers_refuse_buffers_the_kernels_would_overrun():
     sorted_ids, eids, ntpp = ops.align(ids, 16, 16)
     with pytest.raises(ValueError, match="sorted_ids holds"):
         ops.w1_gateup_silu(x, g.experts, sorted_ids[:16], eids, ntpp, top_k=4, path="decode")
+
+
+def test_misaligned_workspace_is_refused():
+    """Workspace sections are read with 16-byte vector and LDS-direct loads at 256-byte offsets
+    from the base: a base off a 256-byte boundary is refused, not run."""
+    from tests.helpers import small_layer, to_gpu
+    g = to_gpu(small_layer(0))
+    x = torch.randn(4, 512, device="cuda").to(torch.bfloat16)
+    need = ops.workspace_bytes(4, 4, g.experts, False, "decode")
+    ws = torch.zeros(need + 256, dtype=torch.uint8, device="cuda")
+    out = ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode", workspace=ws[256:])
+    with pytest.raises(RuntimeError, match="256-byte aligned"):
+        ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode", workspace=ws[4:])
+    torch.cuda.synchronize()
+    want = ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode")
+    assert torch.equal(out, want)
