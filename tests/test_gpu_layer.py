@@ -373,3 +373,16 @@ def test_prefill_router_certificate_on_ties(shared):
         ref = moe_ref.moe_layer_f32(bf16_bits(x), r_ids, r_w, experts_to_np(layer.experts),
                                     shared=experts_to_np(layer.shared), shared_gate_values=sg)
         assert moe_ref.rel_err(out.float().cpu().numpy(), ref) <= LAYER_RTOL
+
+
+@pytest.mark.parametrize("T,path,top_k", [(3, "decode", 8), (3, "decode", 16), (40, "decode", 8),
+                                          (9, "decode", 16), (300, "prefill", 8),
+                                          (1100, "prefill", 8)])
+def test_max_expert_count_with_shared_expert(T, path, top_k):
+    """The largest supported expert set: 512 routed experts plus the shared one (513 groups in
+    align, 513 logits per token in the routers); top-16 in the decode routing, and the
+    large-input align's chunk count at 513 groups for 1100 tokens."""
+    _say(f"512 experts + shared T={T} path={path} top_k={top_k}")
+    layer = synth.make_layer(5, num_experts=512, hidden=512, intermediate=256, zipf=True,
+                             shared=True)
+    _check_layer(layer, T, top_k, path)
