@@ -386,3 +386,14 @@ def test_max_expert_count_with_shared_expert(T, path, top_k):
     layer = synth.make_layer(5, num_experts=512, hidden=512, intermediate=256, zipf=True,
                              shared=True)
     _check_layer(layer, T, top_k, path)
+
+
+@pytest.mark.parametrize("T,path,top_k", [(1, "decode", 1), (7, "decode", 1), (64, "decode", 2),
+                                          (300, "prefill", 1), (1100, "auto", 1),
+                                          (700, "auto", 2)])
+def test_one_and_two_experts_per_token(T, path, top_k):
+    """top_k 1 and 2 (the renormalised weight of a single expert is exactly 1): every routing
+    path, the slot grid and the token-sum W2 included, with a shared expert."""
+    _say(f"top_k={top_k} T={T} path={path}")
+    _check_layer(synth.make_layer(6, num_experts=64, hidden=1024, intermediate=512, zipf=True,
+                                  shared=True), T, top_k, path)
