@@ -124,6 +124,21 @@ int hip_fail(hipError_t e, const char* where) {
     if (_e != hipSuccess) return hip_fail(_e, where); \
   } while (0)
 
+// The calling thread's current device, restored when the guard leaves scope: the handle's
+// calls switch to the cache's device and leave the caller's choice as it was.
+struct DeviceGuard {
+  int prev = -1;
+  DeviceGuard() {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+int setup_live(Cache* c);
+void release_live(Cache* c);
+
 Cache* from_handle(uint64_t h) {
   Cache* c = reinterpret_cast<Cache*>(h);
   if (!c || c->magic != kMagic) return nullptr;
@@ -221,7 +236,37 @@ int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handl
   }
   c->st.capacity = d.slots_per_layer;
   if (live(c)) {
-    SC_HIP(hipSetDevice(d.device), "hipSetDevice");
+    const int rc = setup_live(c);
+    if (rc != MOE_OK) {
+      release_live(c);  // the partial set-up
+      delete c;
+      (void)hipGetLastError();  // the failure is reported here, not at the caller's next HIP call
+      return rc;
+    }
+  }
+  *handle = reinterpret_cast<uint64_t>(c);
+  return MOE_OK;
+}
+
+int moe_slot_cache_destroy_v1(uint64_t handle) {
+  Cache* c = from_handle(handle);
+  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
+  if (live(c)) release_live(c);
+  c->magic = 0;
+  delete c;
+  return MOE_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// HIP objects of a live cache, created on its device (the caller's current device restored).
+int setup_live(Cache* c) {
+  const moe_slot_cache_desc_v1& d = c->d;
+  DeviceGuard guard;
+  SC_HIP(hipSetDevice(d.device), "hipSetDevice");
+  {
     for (hipStream_t& st : c->side)
       SC_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "create copy stream");
     SC_HIP(hipEventCreateWithFlags(&c->compute_mark, hipEventDisableTiming), "create event");
@@ -247,33 +292,32 @@ int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handl
     for (hipEvent_t& e : c->pf_ev) SC_HIP(hipEventCreate(&e), "create timing event");
     for (hipEvent_t& e : c->dm_ev) SC_HIP(hipEventCreate(&e), "create timing event");
   }
-  *handle = reinterpret_cast<uint64_t>(c);
   return MOE_OK;
 }
 
-int moe_slot_cache_destroy_v1(uint64_t handle) {
-  Cache* c = from_handle(handle);
-  if (!c) return fail(MOE_ERR_NULL, "slot cache: bad handle");
-  if (live(c)) {
-    hipSetDevice(c->d.device);
-    // Table uploads from the staging ring and the top-k kernel's flag stores into the signal
-    // words run on the caller's compute stream: wait for the whole device before freeing them.
-    hipDeviceSynchronize();
-    for (hipStream_t st : c->side) hipStreamSynchronize(st);
-    for (hipEvent_t e : c->staging_done) hipEventDestroy(e);
-    for (hipEvent_t e : c->pf_ev) hipEventDestroy(e);
-    for (hipEvent_t e : c->dm_ev) hipEventDestroy(e);
-    hipEventDestroy(c->compute_mark);
-    for (hipStream_t st : c->side) hipStreamDestroy(st);
-    hipHostFree(c->staging);
-    if (c->signal) hipHostFree(c->signal);
-  }
-  c->magic = 0;
-  delete c;
-  return MOE_OK;
+// Frees whatever setup_live created (null members are skipped), on the cache's device.
+void release_live(Cache* c) {
+  DeviceGuard guard;
+  (void)hipSetDevice(c->d.device);
+  // Table uploads from the staging ring and the top-k kernel's flag stores into the signal
+  // words run on the caller's compute stream: wait for the whole device before freeing them.
+  (void)hipDeviceSynchronize();
+  for (hipStream_t st : c->side)
+    if (st) (void)hipStreamSynchronize(st);
+  for (hipEvent_t e : c->staging_done)
+    if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->pf_ev)
+    if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->dm_ev)
+    if (e) (void)hipEventDestroy(e);
+  if (c->compute_mark) (void)hipEventDestroy(c->compute_mark);
+  for (hipStream_t st : c->side)
+    if (st) (void)hipStreamDestroy(st);
+  if (c->staging) (void)hipHostFree(c->staging);
+  if (c->signal) (void)hipHostFree(c->signal);
 }
 
-}  // extern "C"
+}  // namespace
 
 namespace {
 

@@ -543,3 +543,28 @@ def test_offload_decoder_rechecks_replaced_routers_and_top_k():
         check(2)
     finally:
         pool.close()
+
+
+def test_slot_cache_creation_error_leaves_no_state_behind():
+    """A live cache on a device that does not exist is refused when its streams are set up; the
+    partial set-up is released and the caller's current device is unchanged, so a valid cache
+    created next works."""
+    from mtp_amd import _lib
+    from mtp_amd.offload import SlotCache
+    dev_before = torch.cuda.current_device()
+    host = torch.zeros(2 * 64, dtype=torch.uint8).pin_memory()
+    pool = torch.zeros(2 * 64, dtype=torch.uint8, device="cuda")
+    table = torch.full((2,), -1, dtype=torch.int32, device="cuda")
+    with pytest.raises(_lib.MoeLibraryError, match="hipSetDevice"):
+        SlotCache(1, 2, 2, 64, host_pool=host.data_ptr(), device_pool=pool.data_ptr(),
+                  expert_row=table.data_ptr(), device=torch.cuda.device_count() + 3)
+    assert torch.cuda.current_device() == dev_before
+    cache = SlotCache(1, 2, 2, 64, host_pool=host.data_ptr(), device_pool=pool.data_ptr(),
+                      expert_row=table.data_ptr(), device=dev_before)
+    try:
+        assert cache.demand(0, [1]) == 0
+        torch.cuda.synchronize()
+        assert cache.slot_of(0, 1) >= 0
+    finally:
+        cache.close()
+    assert torch.cuda.current_device() == dev_before
