@@ -25,7 +25,10 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// The error is reported through the return code and the message; the thread's last HIP error
+// is cleared so that it does not surface again at the caller's next, unrelated HIP call.
 int hip_fail(hipError_t e, const char* where) {
+  (void)hipGetLastError();
   return fail(MOE_ERR_HIP + ((int)e % 100), "%s: HIP error %d (%s)", where, (int)e,
               hipGetErrorString(e));
 }

@@ -31,6 +31,7 @@ int scratch_for_current_device(void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
+    (void)hipGetLastError();  // reported here, not at the caller's next HIP call
     snprintf(moe_error_buffer(), kErrorBufferBytes, "noalloc: hipGetDevice: HIP error %d (%s)",
              (int)e, hipGetErrorString(e));
     return MOE_ERR_HIP + ((int)e % 100);
@@ -45,6 +46,7 @@ int scratch_for_current_device(void** out) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
       snprintf(moe_error_buffer(), kErrorBufferBytes,
                "noalloc: hipGetSymbolAddress(scratch) on device %d: HIP error %d (%s)", dev,
                (int)e, hipGetErrorString(e));

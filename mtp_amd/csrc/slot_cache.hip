@@ -112,7 +112,9 @@ int fail(int code, const char* msg) {
   return code;
 }
 
+// Reported through the return code and the message; the thread's last HIP error is cleared.
 int hip_fail(hipError_t e, const char* where) {
+  (void)hipGetLastError();
   snprintf(moe_error_buffer(), kErrorBufferBytes, "%s: HIP error %d (%s)", where, (int)e,
            hipGetErrorString(e));
   return MOE_ERR_HIP + ((int)e % 100);
@@ -240,7 +242,7 @@ int moe_slot_cache_create_v1(const moe_slot_cache_desc_v1* desc, uint64_t* handl
     if (rc != MOE_OK) {
       release_live(c);  // the partial set-up
       delete c;
-      (void)hipGetLastError();  // the failure is reported here, not at the caller's next HIP call
+      (void)hipGetLastError();  // release_live's own calls on the failed device
       return rc;
     }
   }
