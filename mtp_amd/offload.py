@@ -341,17 +341,19 @@ def routed_layer(x: torch.Tensor, router_w: torch.Tensor, pool: OffloadedExperts
     ops._require_gpu(x, router_w, logit_bias)
     T = x.shape[0]
     p = ops._path(path)
-    need = ops.workspace_bytes(T, top_k, ex, False, p)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    workspace = ops._workspace(workspace, ops.workspace_bytes(T, top_k, ex, False, p), x.device)
     if ids_host is None or tuple(ids_host.shape) != (T, top_k):
         ids_host = torch.empty((T, top_k), dtype=torch.int32, pin_memory=True)
+    elif (ids_host.device.type != "cpu" or ids_host.dtype != torch.int32
+          or not ids_host.is_contiguous()):
+        # the cache's demand reads the routed ids on the host
+        raise ValueError("ids_host must be a contiguous int32 CPU tensor")
     out = torch.empty_like(x)
     arr, n = SlotCache._ids(prefetch or [])
     st = ex.struct()
     _lib.check(lib.moe_offload_layer_v1(
         pool.cache.handle, layer, x.data_ptr(), T, router_w.data_ptr(), ops._ptr(logit_bias),
-        top_k, ctypes.byref(st), workspace.data_ptr(), workspace.numel(), out.data_ptr(),
+        top_k, ctypes.byref(st), workspace.data_ptr(), ops._nbytes(workspace), out.data_ptr(),
         ids_host.data_ptr(), arr, n, p, ops._stream(), None))
     return out, ids_host
 

@@ -51,6 +51,21 @@ def _require_experts_on(device: torch.device, *sets: MoeExperts | None) -> None:
             raise ValueError(f"expert weights on {ex.device}, activations on {device}")
 
 
+def _workspace(workspace: torch.Tensor | None, need: int, device: torch.device) -> torch.Tensor:
+    """The caller's workspace when it is a contiguous tensor on ``device`` of at least ``need``
+    bytes; a smaller one is replaced by a new allocation."""
+    if workspace is not None:
+        if not workspace.is_cuda or workspace.device != device or not workspace.is_contiguous():
+            raise ValueError(f"workspace must be a contiguous tensor on {device}")
+        if _nbytes(workspace) >= need:
+            return workspace
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
 def _path(path: str | int) -> int:
     if isinstance(path, int):
         return path
@@ -244,6 +259,7 @@ def w2_down(h, experts: MoeExperts, sorted_ids, expert_ids, ntpp, topk_weights_f
     elif (ys.dtype != torch.float32 or tuple(ys.shape) != (h.shape[0], experts.hidden_size)
           or not ys.is_contiguous()):
         raise ValueError("ys must be contiguous float32 [slots, hidden]")
+    _require_gpu(h, ys)
     ex = experts.struct()
     sh = shared.struct() if shared is not None else None
     _lib.check(lib.moe_w2_down_v1(
@@ -264,7 +280,8 @@ def moe_sum(ys: torch.Tensor, topk_ids: torch.Tensor, experts: MoeExperts,
     _require_gpu(ys, topk_ids)
     T, top_k = topk_ids.shape
     H = ys.shape[1]
-    if ys.dtype != torch.float32 or ys.shape[0] < T * top_k + (T if has_shared else 0):
+    if (ys.dtype != torch.float32 or ys.ndim != 2
+            or ys.shape[0] < T * top_k + (T if has_shared else 0)):
         raise ValueError("ys must be float32 [T*k (+T), H]")
     out = torch.empty(T, H, dtype=torch.bfloat16, device=ys.device)
     _lib.check(lib.moe_sum_v1(ys.data_ptr(), T, top_k, H, int(has_shared), topk_ids.data_ptr(),
@@ -294,6 +311,7 @@ def rmsnorm(res: torch.Tensor, weight: torch.Tensor, *, add: torch.Tensor | None
         out = torch.empty_like(res)
     elif out.shape != res.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("out must be a contiguous bf16 tensor shaped like res")
+    _require_gpu(res, out)
     _lib.check(lib.moe_rmsnorm_v1(res.data_ptr(), _ptr(add), T, H, weight.data_ptr(), float(eps),
                                   out.data_ptr(), _stream()))
     return out
@@ -328,13 +346,13 @@ def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, t
     _require_experts_on(x.device, experts, shared)
     T = x.shape[0]
     p = _path(path)
-    need = workspace_bytes(T, top_k, experts, shared is not None, p)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    workspace = _workspace(workspace, workspace_bytes(T, top_k, experts, shared is not None, p),
+                           x.device)
     if out is None:
         out = torch.empty_like(x)
     elif out.shape != x.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("out must be a contiguous bf16 tensor shaped like the input")
+    _require_gpu(x, out)
     ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device) if return_routing else None
     w = torch.empty(T, top_k, dtype=torch.float32, device=x.device) if return_routing else None
     ex = experts.struct()
@@ -342,7 +360,7 @@ def moe_layer(x: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts, *, t
     _lib.check(lib.moe_layer_v1(
         x.data_ptr(), T, router_w.data_ptr(), _ptr(logit_bias), top_k, ctypes.byref(ex),
         ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
-        workspace.numel(), out.data_ptr(), _ptr(ids), _ptr(w), p, _stream()))
+        _nbytes(workspace), out.data_ptr(), _ptr(ids), _ptr(w), p, _stream()))
     if return_routing:
         return out, ids, w
     return out
@@ -372,7 +390,8 @@ def norm_layer(res: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts,
     if (shared is None) != (shared_gate_w is None):
         raise ValueError("shared and shared_gate_w must be given together")
     _check_bias_gate(logit_bias, shared_gate_w, experts.num_experts, experts.hidden_size)
-    _require_gpu(res, add, norm_w, router_w)
+    _require_gpu(res, add, norm_w, router_w, logit_bias, shared_gate_w)
+    _require_experts_on(res.device, experts, shared)
     if res_out is None:
         res_out = torch.empty_like(res)
     if x_out is None:
@@ -382,17 +401,17 @@ def norm_layer(res: torch.Tensor, router_w: torch.Tensor, experts: MoeExperts,
     for t, name in ((res_out, "res_out"), (x_out, "x_out"), (out, "out")):
         if t.shape != res.shape or t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous bf16 tensor shaped like res")
+    _require_gpu(res, res_out, x_out, out)
     p = _path(path)
-    need = workspace_bytes(T, top_k, experts, shared is not None, p)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=res.device)
+    workspace = _workspace(workspace, workspace_bytes(T, top_k, experts, shared is not None, p),
+                           res.device)
     ex = experts.struct()
     sh = shared.struct() if shared is not None else None
     _lib.check(lib.moe_norm_layer_v1(
         res.data_ptr(), _ptr(add), norm_w.data_ptr(), float(eps), res_out.data_ptr(),
         x_out.data_ptr(), T, router_w.data_ptr(), _ptr(logit_bias), top_k, ctypes.byref(ex),
         ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
-        workspace.numel(), out.data_ptr(), None, None, p, _stream()))
+        _nbytes(workspace), out.data_ptr(), None, None, p, _stream()))
     return out, res_out, x_out
 
 
@@ -414,16 +433,15 @@ def fused_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.T
     _require_experts_on(x.device, experts, shared)
     T, k = topk_ids.shape
     p = _path(path)
-    need = workspace_bytes(T, k, experts, shared is not None, p)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    workspace = _workspace(workspace, workspace_bytes(T, k, experts, shared is not None, p),
+                           x.device)
     out = torch.empty_like(x)
     ex = experts.struct()
     sh = shared.struct() if shared is not None else None
     _lib.check(lib.moe_fused_experts_v1(
         x.data_ptr(), T, topk_ids.data_ptr(), topk_weights.data_ptr(), k, ctypes.byref(ex),
         ctypes.byref(sh) if sh else None, _ptr(shared_gate_w), workspace.data_ptr(),
-        workspace.numel(), out.data_ptr(), p, _stream()))
+        _nbytes(workspace), out.data_ptr(), p, _stream()))
     return out
 
 
@@ -460,14 +478,14 @@ def predictor_topk(h: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, top_k: i
             raise TypeError(f"{name} must be contiguous bf16")
     _require_gpu(h, w1, w2)
     T = h.shape[0]
-    need = predictor_workspace_bytes(T, L, D, E, top_k)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=h.device)
+    # a negative size (invalid sizes) leaves the error to the entry point's own checks
+    workspace = _workspace(workspace, predictor_workspace_bytes(T, L, D, E, top_k), h.device)
     if out is None:
         out = torch.empty(L, T, top_k, dtype=torch.int32, device=h.device)
     elif out.dtype != torch.int32 or out.shape != (L, T, top_k) or not out.is_contiguous():
         raise ValueError("out must be contiguous int32 [L, T, top_k]")
+    _require_gpu(h, out)
     _lib.check(lib.moe_predictor_v1(h.data_ptr(), T, H, L, w1.data_ptr(), D, w2.data_ptr(), E,
-                                    top_k, workspace.data_ptr(), workspace.numel(),
+                                    top_k, workspace.data_ptr(), _nbytes(workspace),
                                     out.data_ptr(), _stream()))
     return out

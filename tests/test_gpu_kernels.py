@@ -203,3 +203,48 @@ def test_misaligned_workspace_is_refused():
     torch.cuda.synchronize()
     want = ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode")
     assert torch.equal(out, want)
+
+
+def test_caller_buffers_off_the_device_or_strided_are_refused():
+    """The C ABI sees a caller's workspace and outputs only as pointers and byte counts: a host
+    tensor, one on another device or an expanded (stride-0) one is refused by the wrappers, and
+    a workspace of another dtype counts its bytes, not its elements."""
+    _say("caller buffer checks")
+    from tests.helpers import small_layer, to_gpu
+    g = to_gpu(small_layer(0))
+    x = torch.randn(4, 512, device="cuda").to(torch.bfloat16)
+    need = ops.workspace_bytes(4, 4, g.experts, False, "decode")
+    want = ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode")
+    for ws in (torch.empty(need, dtype=torch.uint8),
+               torch.empty(1, dtype=torch.uint8, device="cuda").expand(need)):
+        with pytest.raises(ValueError, match="workspace must be a contiguous tensor"):
+            ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode", workspace=ws)
+        with pytest.raises(ValueError, match="workspace must be a contiguous tensor"):
+            ops.fused_experts(x, torch.zeros(4, 4, dtype=torch.int32, device="cuda"),
+                              torch.zeros(4, 4, device="cuda"), g.experts, path="decode",
+                              workspace=ws)
+    with pytest.raises(ValueError, match="CPU tensor"):
+        ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode",
+                      out=torch.empty(4, 512, dtype=torch.bfloat16))
+    norm_w = torch.zeros(512, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="CPU tensor"):
+        ops.norm_layer(x, g.router_w, g.experts, norm_w, top_k=4, path="decode",
+                       x_out=torch.empty(4, 512, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="CPU tensor"):
+        ops.rmsnorm(x.clone(), norm_w, out=torch.empty(4, 512, dtype=torch.bfloat16))
+    ids, w, _, _ = ops.router_topk(x, g.router_w, 4)
+    sorted_ids, eids, ntpp = ops.align(ids, 16, ops.DECODE_BLOCK_M)
+    h = ops.w1_gateup_silu(x, g.experts, sorted_ids, eids, ntpp, top_k=4, path="decode")
+    with pytest.raises(ValueError, match="CPU tensor"):
+        ops.w2_down(h, g.experts, sorted_ids, eids, ntpp, w.reshape(-1), T=4, top_k=4,
+                    path="decode", ys=torch.empty(16, 512, dtype=torch.float32))
+    hp = torch.randn(2, 64, device="cuda").to(torch.bfloat16)
+    w1 = torch.zeros(1, 32, 64, dtype=torch.bfloat16, device="cuda")
+    w2 = torch.zeros(1, 16, 32, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="workspace must be a contiguous tensor"):
+        ops.predictor_topk(hp, w1, w2, 4, workspace=torch.empty(1 << 16, dtype=torch.uint8))
+    # float32 elements: a quarter of `need` of them covers the workspace
+    ws32 = torch.empty((need + 3) // 4, dtype=torch.float32, device="cuda")
+    got = ops.moe_layer(x, g.router_w, g.experts, top_k=4, path="decode", workspace=ws32)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

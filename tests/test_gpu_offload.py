@@ -148,6 +148,19 @@ def test_offload_layer_ids_reach_any_host_buffer(pooled, where):
         assert bool((big[:13] == -7).all()) and bool((big[13 + T * 4:] == -7).all())
 
 
+def test_offload_layer_refuses_device_or_mistyped_ids_buffers(pooled):
+    """The cache's demand reads the routed ids on the host: an ids buffer in device memory or of
+    another dtype is refused before any call."""
+    layers, pool = pooled
+    g = layers[0]
+    x = synth.make_tokens(3, 512, seed=124).cuda()
+    for buf in (torch.zeros(3, 4, dtype=torch.int32, device="cuda"),
+                torch.zeros(3, 4, dtype=torch.int64)):
+        with pytest.raises(ValueError, match="ids_host"):
+            routed_layer(x, g.router_w, pool, 0, top_k=4, logit_bias=g.logit_bias,
+                         ids_host=buf, path="decode")
+
+
 @pytest.mark.parametrize("T,L,H,D,E,k", [(1, 3, 512, 256, 64, 16), (4, 2, 2048, 1024, 256, 16),
                                           (3, 1, 256, 64, 40, 5)])
 def test_predictor_matches_oracle(T, L, H, D, E, k):
