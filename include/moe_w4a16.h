@@ -120,7 +120,8 @@ int moe_capacity_blocks_v1(int32_t T, int32_t top_k, int32_t num_experts, int32_
  * (src/mtp_expert_prefetch/tracing/vllm_router_trace.py:19647-19660; format pinned by
  * tests/test_vllm_descriptor_mapping_assertion.py:1012-1085).
  * sorted_ids int32 [capacity_blocks*block_m]; expert_ids int32 [capacity_blocks] (-1 for
- * unused blocks); ntpp int32 [1]. Slots whose id is outside [0, E) are dropped. */
+ * unused blocks); ntpp int32 [1]. Slots whose id is outside [0, E) are dropped. With T = 0
+ * and capacity_blocks = 0 only ntpp (0) is written, and sorted_ids/expert_ids may be NULL. */
 int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_experts,
                  int32_t has_shared, int32_t block_m, int32_t capacity_blocks,
                  int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, void* stream);

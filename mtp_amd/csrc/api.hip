@@ -354,9 +354,11 @@ int moe_capacity_blocks_v1(int32_t T, int32_t top_k, int32_t num_experts, int32_
 int moe_align_v1(const int32_t* topk_ids, int32_t T, int32_t top_k, int32_t num_experts,
                  int32_t has_shared, int32_t block_m, int32_t capacity_blocks,
                  int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, void* stream) {
-  if (!sorted_ids || !expert_ids || !ntpp || (T > 0 && !topk_ids))
+  // No tokens and no capacity: only ntpp (0) is written, and the empty tables may be NULL.
+  if (!ntpp || (capacity_blocks > 0 && (!sorted_ids || !expert_ids)) || (T > 0 && !topk_ids))
     return fail(MOE_ERR_NULL, "align: NULL pointer");
   if (T < 0 || top_k < 1 || top_k > 64) return fail(MOE_ERR_SHAPE, "align: T=%d top_k=%d", T, top_k);
+  if (capacity_blocks < 0) return fail(MOE_ERR_SHAPE, "align: capacity_blocks=%d", capacity_blocks);
   if (num_experts < 1 || num_experts > 512)
     return fail(MOE_ERR_SHAPE, "align: num_experts=%d outside [1, 512]", num_experts);
   if (block_m < 1 || block_m > 1024) return fail(MOE_ERR_SHAPE, "align: block_m=%d", block_m);

@@ -9,6 +9,7 @@ vLLM's topk_softmax(renormalize=True) (src/mtp_expert_prefetch/tracing/vllm_rout
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import torch
@@ -73,10 +74,11 @@ class MoeBlock(torch.nn.Module):
                              f"got {tuple(expert_ids.shape)} and {tuple(hidden_states.shape)}")
         flat = self._flat(hidden_states)
         T = flat.shape[0]
-        ids = expert_ids.reshape(T, -1).to(device=flat.device, dtype=torch.int32).contiguous()
+        k = math.prod(expert_ids.shape[2:])  # ids per token (the reference's reshape(T, -1))
+        ids = expert_ids.reshape(T, k).to(device=flat.device, dtype=torch.int32).contiguous()
         if bool(((ids < 0) | (ids >= self.num_experts)).any()):
             raise KeyError(f"expert ids must lie in [0, {self.num_experts})")
-        w = expert_weights.reshape(T, -1).to(device=flat.device, dtype=torch.float32).contiguous()
+        w = expert_weights.reshape(T, k).to(device=flat.device, dtype=torch.float32).contiguous()
         out = ops.fused_experts(flat, ids, w, self.experts, shared=self.shared_expert,
                                 shared_gate_w=self.shared_expert_gate_weight)
         return out.reshape(hidden_states.shape)

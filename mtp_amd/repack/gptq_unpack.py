@@ -250,6 +250,7 @@ def _as_quantized(weights) -> QuantizedExpertWeights:
 
 
 _KINDS = ("qweight", "qzeros", "scales")
+_MAX_IDS_PER_CALL = 64  # experts per token that one fused-experts call accepts
 
 
 class _Int4ExpertStack(torch.nn.Module):
@@ -369,12 +370,21 @@ class _Int4ExpertStack(torch.nn.Module):
         x = input_tensor.reshape(-1, self.hidden_size).to(device=dev, dtype=torch.bfloat16)
         x = x.contiguous()
         T, k = x.shape[0], len(rows)
+        if k == 0:  # the reference's sum over no experts is its zero start value
+            return torch.zeros_like(input_tensor)
         ids = torch.tensor(rows, dtype=torch.int32, device=dev).expand(T, k).contiguous()
         if weights is None:
             w = torch.ones(T, k, dtype=torch.float32, device=dev)
         else:
             w = weights.to(device=dev, dtype=torch.float32).expand(T, k).contiguous()
-        out = ops.fused_experts(x, ids, w, experts)
+        if k <= _MAX_IDS_PER_CALL:
+            out = ops.fused_experts(x, ids, w, experts)
+        else:  # the kernels take up to 64 experts per token: sum the chunks' outputs in fp32
+            out = torch.zeros(T, self.hidden_size, dtype=torch.float32, device=dev)
+            for lo in range(0, k, _MAX_IDS_PER_CALL):
+                hi = min(lo + _MAX_IDS_PER_CALL, k)
+                out += ops.fused_experts(x, ids[:, lo:hi].contiguous(), w[:, lo:hi].contiguous(),
+                                         experts).float()
         return out.to(device=home, dtype=input_tensor.dtype).reshape(input_tensor.shape)
 
 

@@ -69,6 +69,27 @@ def test_topk_expert_mlp_weighted_sum(store_dir):
         mlp(x.cuda(), ids.view(1, 2), w.view(1, 2))
 
 
+def test_topk_expert_mlp_with_no_ids_and_with_more_than_64(store_dir):
+    """The reference sums the listed experts one after another from zeros
+    (gptq_unpack.py:318-326): no ids give zeros, and any number of ids is summed (the
+    kernels take 64 experts per token per call; longer lists are summed in chunks)."""
+    d, ex = store_dir
+    with RepackedMoeExpertStore(d) as store:
+        mlp = load_topk_expert_mlp(store, layer=0, expert_ids=list(range(E)), device="cuda")
+    x = synth.make_tokens(5, H, seed=9)
+    none = mlp(x.cuda(), torch.empty(0, dtype=torch.long), torch.empty(0))
+    assert none.shape == (5, H) and not bool(none.any())
+    rng = np.random.default_rng(4)
+    ids_np = rng.integers(0, E, 150).astype(np.int32)
+    w_np = rng.uniform(0.001, 0.01, 150).astype(np.float32)
+    out = mlp(x.cuda(), torch.from_numpy(ids_np).long(), torch.from_numpy(w_np).cuda())
+    # the module casts the weights to the input's dtype (bf16) first, as the reference does
+    w_bf = torch.from_numpy(w_np).to(torch.bfloat16).float().numpy()
+    ref = moe_ref.moe_layer_f32(bf16_bits(x), np.tile(ids_np, (5, 1)), np.tile(w_bf, (5, 1)),
+                                experts_to_np(ex))
+    assert moe_ref.rel_err(out.float().cpu().numpy(), ref) <= LAYER_RTOL
+
+
 def test_single_expert_mlp(store_dir):
     d, ex = store_dir
     with RepackedMoeExpertStore(d) as store:

@@ -132,6 +132,41 @@ def test_fused_experts_and_moe_tokens_api():
         block.moe_tokens(x.cuda().view(2, 3, 512), torch.full((2, 3, k), 99), torch.from_numpy(w).view(2, 3, k))
 
 
+def test_empty_batch_gives_empty_outputs():
+    """A batch of no tokens is a no-op of every layer entry point (T = 0 returns at once; align
+    writes only ntpp = 0 and takes NULL tables); the shapes come back empty."""
+    _say("empty batch")
+    g = to_gpu(small_layer(3, shared=True))
+    sh = dict(shared=g.shared, shared_gate_w=g.shared_gate_w)
+    x = torch.empty(0, 512, dtype=torch.bfloat16, device="cuda")
+    for path in ("auto", "decode", "prefill"):
+        out, ids, w = ops.moe_layer(x, g.router_w, g.experts, top_k=4, path=path,
+                                    return_routing=True, **sh)
+        assert out.shape == (0, 512) and ids.shape == (0, 4) and w.shape == (0, 4)
+    r_ids, r_w, gate, logits = ops.router_topk(x, g.router_w, 4, shared_gate_w=g.shared_gate_w)
+    assert r_ids.shape == (0, 4) and r_w.shape == (0, 4) and gate.shape == (0,)
+    assert logits.shape == (0, 16)
+    sorted_ids, eids, ntpp = ops.align(r_ids, 16, ops.DECODE_BLOCK_M, has_shared=True)
+    assert sorted_ids.numel() == 0 and eids.numel() == 0
+    h = ops.w1_gateup_silu(x, g.experts, sorted_ids, eids, ntpp, top_k=4, shared=g.shared,
+                           path="decode")
+    ys = ops.w2_down(h, g.experts, sorted_ids, eids, ntpp, r_w.reshape(-1), T=0, top_k=4,
+                     shared=g.shared, path="decode")
+    assert h.shape == (0, 256) and ys.shape == (0, 512)
+    assert ops.moe_sum(ys, r_ids, g.experts, has_shared=True).shape == (0, 512)
+    assert ops.fused_experts(x, r_ids, r_w, g.experts, **sh).shape == (0, 512)
+    norm_w = torch.zeros(512, dtype=torch.bfloat16, device="cuda")
+    out, res_out, xn = ops.norm_layer(x, g.router_w, g.experts, norm_w, top_k=4, **sh)
+    assert out.shape == res_out.shape == xn.shape == (0, 512)
+    block = MoeBlock(g.experts, g.router_w, shared_expert=g.shared,
+                     shared_expert_gate_weight=g.shared_gate_w, top_k=4)
+    assert block(x.view(2, 0, 512)).shape == (2, 0, 512)
+    assert block.moe_tokens(x.view(2, 0, 512), torch.empty(2, 0, 4, dtype=torch.long),
+                            torch.empty(2, 0, 4)).shape == (2, 0, 512)
+    torch.cuda.synchronize()
+    assert int(ntpp.item()) == 0
+
+
 def test_expert_row_indirection_matches_direct():
     """A slot pool: experts held in arbitrary rows, addressed through expert_row."""
     _say("expert_row indirection")
