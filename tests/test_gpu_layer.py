@@ -432,3 +432,16 @@ def test_one_and_two_experts_per_token(T, path, top_k):
     _say(f"top_k={top_k} T={T} path={path}")
     _check_layer(synth.make_layer(6, num_experts=64, hidden=1024, intermediate=512, zipf=True,
                                   shared=True), T, top_k, path)
+
+
+@pytest.mark.parametrize("T,path,top_k", [(1, "decode", 16), (3, "decode", 64), (40, "decode", 16),
+                                          (9, "decode", 32), (20, "prefill", 64),
+                                          (300, "prefill", 16), (100, "auto", 64)])
+def test_many_experts_per_token(T, path, top_k):
+    """top_k up to the entry points' limit of 64 (64 = every expert of the layer), with a shared
+    expert: the selection rounds past 8, the block-routed decode kernels (the slot grid and the
+    token-sum W2 take at most 8), the sum over more than 8 rows per token, and at prefill the
+    certified top-k and the large-input align (4 800 and 6 500 slots)."""
+    _say(f"top_k={top_k} T={T} path={path}")
+    _check_layer(synth.make_layer(7, num_experts=64, hidden=1024, intermediate=512, zipf=True,
+                                  shared=True), T, top_k, path)
