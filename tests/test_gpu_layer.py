@@ -445,3 +445,14 @@ def test_many_experts_per_token(T, path, top_k):
     _say(f"top_k={top_k} T={T} path={path}")
     _check_layer(synth.make_layer(7, num_experts=64, hidden=1024, intermediate=512, zipf=True,
                                   shared=True), T, top_k, path)
+
+
+@pytest.mark.parametrize("T,shared", [(4096, False), (4096, True), (8192, False)])
+def test_prefill_batches_past_the_large_input_align(T, shared):
+    """Prefill batches of 4 096 and 8 192 tokens (top-8, 64 experts, the hottest routed by
+    nearly every token): 32 768 slots are the largest the many-workgroup align takes, and above
+    it (36 864 and 65 536 slots) the one-workgroup align runs and the GEMMs take the blocks in
+    align order."""
+    _say(f"prefill T={T} shared={shared}")
+    _check_layer(synth.make_layer(8, num_experts=64, hidden=512, intermediate=256, zipf=True,
+                                  shared=shared), T, 8, "prefill")
