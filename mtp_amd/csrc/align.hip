@@ -343,30 +343,28 @@ int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM) {
 }
 
 namespace {
-// Chunks of the two-kernel align, or 0 when the input takes the one-block kernel: large inputs
-// with room for the scratch in the sorted buffer.
-int align_chunks(int T, int top_k, int E, int has_shared, int BM, int cap, int* CH) {
+// Chunks of the two-kernel align, or 0 when the input takes the one-block kernel: large inputs.
+// With a scratch buffer of its own (the scatter form) any number of slots; otherwise the ranks and
+// counts go into the sorted buffer, which needs room for them, and the finish kernel holds at most
+// kAlign2MaxSlotsPerThread slots per thread.
+int align_chunks(int T, int top_k, int E, int has_shared, int BM, int cap, bool scratch, int* CH) {
   const int n_slots = T * top_k + (has_shared ? T : 0);
   const int G = E + (has_shared ? 1 : 0);
   int nchunks = kAlign2LdsCounts / G;
   if (nchunks > kAlign2MaxChunks) nchunks = kAlign2MaxChunks;
-  if (n_slots < 4096 || BM < 64 || BM > 16 * kOrderMaxClasses || nchunks <= 0 ||
-      n_slots > 1024 * kAlign2MaxSlotsPerThread || G > kMaxGroups ||
-      (int64_t)cap * BM < (int64_t)n_slots + (int64_t)nchunks * G)
+  if (n_slots < 4096 || BM < 64 || BM > 16 * kOrderMaxClasses || nchunks <= 0 || G > kMaxGroups)
+    return 0;
+  if (!scratch && (n_slots > 1024 * kAlign2MaxSlotsPerThread ||
+                   (int64_t)cap * BM < (int64_t)n_slots + (int64_t)nchunks * G))
     return 0;
   *CH = ((n_slots + nchunks - 1) / nchunks + 63) / 64 * 64;
   return (n_slots + *CH - 1) / *CH;
 }
 }  // namespace
 
-bool align_orders_blocks(int T, int top_k, int E, int has_shared, int BM, int cap) {
-  int CH = 0;
-  return align_chunks(T, top_k, E, has_shared, BM, cap, &CH) > 0;
-}
-
 int64_t align_scratch_bytes(int T, int top_k, int E, int has_shared, int BM, int cap) {
   int CH = 0;
-  const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, &CH);
+  const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, true, &CH);
   if (nchunks <= 0) return 0;
   const int64_t n_slots = (int64_t)T * top_k + (has_shared ? T : 0);
   return (n_slots + (int64_t)nchunks * (E + (has_shared ? 1 : 0))) * 4;
@@ -376,7 +374,7 @@ hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int ha
                         int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
                         int32_t* scratch, hipStream_t stream) {
   int CH = 0;
-  const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, &CH);
+  const int nchunks = align_chunks(T, top_k, E, has_shared, BM, cap, scratch != nullptr, &CH);
   if (nchunks > 0 && scratch) {
     hipLaunchKernelGGL(align_chunk_kernel, dim3(nchunks), dim3(64), 0, stream, topk_ids, T,
                        top_k, E, has_shared, CH, scratch);

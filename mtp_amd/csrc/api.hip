@@ -175,11 +175,15 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   int32_t* ntpp = at<int32_t>(ws, L.ntpp);
   uint16_t* h = at<uint16_t>(ws, L.h);
   float* ys = at<float>(ws, L.ys);
-  // the large-input align also orders the blocks for the prefill GEMMs
-  int32_t* border = routing == ROUTE_ALIGN && path == MOE_PATH_PREFILL &&
-                            align_orders_blocks(T, top_k, ex->num_experts, has_shared, L.bm, L.cap)
-                        ? at<int32_t>(ws, L.border)
-                        : nullptr;
+  // The large-input align keeps its ranks and chunk counts in the ys section (not in use until
+  // W2) and also orders the blocks for the prefill GEMMs.
+  int32_t* scratch = nullptr;
+  if (routing == ROUTE_ALIGN) {
+    const int64_t scratch_bytes =
+        align_scratch_bytes(T, top_k, ex->num_experts, has_shared, L.bm, L.cap);
+    if (scratch_bytes > 0 && (size_t)scratch_bytes <= L.total - L.ys) scratch = at<int32_t>(ws, L.ys);
+  }
+  int32_t* border = scratch && path == MOE_PATH_PREFILL ? at<int32_t>(ws, L.border) : nullptr;
   const bool grid = routing == ROUTE_GRID_LOGITS || routing == ROUTE_GRID_IDS;
   if (grid) {
     const SlotGrid sg{1, routing == ROUTE_GRID_LOGITS ? at<float>(ws, L.logits) : nullptr, ids, w};
@@ -196,13 +200,6 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
     MOE_CHECK_HIP(launch_w1_decode_slotgrid(x, ed, sd, sg, h, stream), "w1 (slot grid)");
   } else {
     if (routing == ROUTE_ALIGN) {
-      // the ys section is not in use until W2: the large-input align keeps its ranks and
-      // chunk counts there
-      const int64_t scratch_bytes =
-          align_scratch_bytes(T, top_k, ex->num_experts, has_shared, L.bm, L.cap);
-      int32_t* scratch = scratch_bytes > 0 && (size_t)scratch_bytes <= L.total - L.ys
-                             ? at<int32_t>(ws, L.ys)
-                             : nullptr;
       MOE_CHECK_HIP(launch_align(ids, T, top_k, ex->num_experts, has_shared, L.bm, L.cap, sorted,
                                  eids, ntpp, border, scratch, stream), "align");
     }

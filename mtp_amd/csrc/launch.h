@@ -73,13 +73,14 @@ hipError_t launch_shared_gate(const uint16_t* x, int T, int H, const uint16_t* s
                               int top_k, float* logits_ws, float* weights, hipStream_t stream);
 
 int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM);
-// Whether launch_align writes `border` for these sizes (the large-input path): the align blocks
-// sorted by the number of 16-row subtiles holding slots, heaviest first (cap entries at most).
-bool align_orders_blocks(int T, int top_k, int E, int has_shared, int BM, int cap);
 // Bytes of scratch (outside the output buffers) that lets launch_align spread the large-input
-// scatter over many workgroups; 0 when these sizes take the one-block kernel.
+// scatter over many workgroups, for any number of slots; 0 when these sizes take the one-block
+// kernel. Given such a scratch, launch_align also writes `border` (when non-null): the align
+// blocks sorted by the number of 16-row subtiles holding slots, heaviest first (cap entries).
 int64_t align_scratch_bytes(int T, int top_k, int E, int has_shared, int BM, int cap);
-// scratch (nullable): align_scratch_bytes bytes the call may overwrite.
+// scratch (nullable): align_scratch_bytes bytes the call may overwrite. Without it, inputs of up to
+// 32 768 slots still take a two-kernel form (ranks and counts in the sorted buffer), larger ones the
+// one-block kernel.
 hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int has_shared, int BM,
                         int cap, int32_t* sorted, int32_t* eids, int32_t* ntpp, int32_t* border,
                         int32_t* scratch, hipStream_t stream);
@@ -144,7 +145,7 @@ hipError_t launch_w2_token_sum(const uint16_t* h, const ExpertsDev& ed, const Sl
                                const int32_t* ids, const float* topk_w, uint16_t* out,
                                hipStream_t stream);
 
-// Prefill (bf16 MFMA) path. border (nullable): the block order of align_orders_blocks.
+// Prefill (bf16 MFMA) path. border (nullable): the block order written by the large-input align.
 hipError_t launch_w1_prefill(const uint16_t* x, const ExpertsDev& ed, const SlotsDev& sd,
                              const int32_t* sorted, const int32_t* eids, const int32_t* ntpp,
                              const int32_t* border, int BM, int cap, uint16_t* h,

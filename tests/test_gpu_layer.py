@@ -450,9 +450,9 @@ def test_many_experts_per_token(T, path, top_k):
 @pytest.mark.parametrize("T,shared", [(4096, False), (4096, True), (8192, False)])
 def test_prefill_batches_past_the_large_input_align(T, shared):
     """Prefill batches of 4 096 and 8 192 tokens (top-8, 64 experts, the hottest routed by
-    nearly every token): 32 768 slots are the largest the many-workgroup align takes, and above
-    it (36 864 and 65 536 slots) the one-workgroup align runs and the GEMMs take the blocks in
-    align order."""
+    nearly every token): 32 768, 36 864 and 65 536 slots through the layer call's many-workgroup
+    align (its ranks and chunk counts in the workspace, the GEMMs' block order written beside
+    the layout), past the 32 768 slots that the standalone align's two-kernel form holds."""
     _say(f"prefill T={T} shared={shared}")
     _check_layer(synth.make_layer(8, num_experts=64, hidden=512, intermediate=256, zipf=True,
                                   shared=shared), T, 8, "prefill")
