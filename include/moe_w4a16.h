@@ -78,7 +78,7 @@ typedef struct moe_expert_set_v1 {
  *            MFMA operand, K split across waves (token batches up to a few hundred slots);
  *   PREFILL: MFMA on 128-slot blocks, activation tiles staged in LDS, int4 dequantised in
  *            registers into the MFMA operand;
- *   AUTO   : PREFILL when T * top_k >= 1024, else DECODE.
+ *   AUTO   : PREFILL when T * top_k >= 2560, else DECODE.
  * Any other value is refused with MOE_ERR_UNSUPPORTED (the workspace query returns -1). */
 enum { MOE_PATH_AUTO = 0, MOE_PATH_DECODE = 1, MOE_PATH_PREFILL = 2 };
 

@@ -15,15 +15,6 @@
 
 namespace {
 
-__global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__ topk_ids, int T,
-                                                     int top_k, int E, int has_shared, int BM,
-                                                     int cap, int32_t* __restrict__ sorted,
-                                                     int32_t* __restrict__ eids,
-                                                     int32_t* __restrict__ ntpp) {
-  __shared__ AlignSmem sm;
-  align_block(topk_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, sm);
-}
-
 // ---- Two-kernel align for large inputs (prefill): chunk ranks in parallel, then one block.
 // Kernel 1: workgroup c (one wave) ranks the slots of chunk c = [c CH, (c + 1) CH) by expert in
 // slot order (the ballot match of align_block, 64 slots at a time) and writes, into the sorted
@@ -126,6 +117,26 @@ MOE_DEV void block_order(const int* s_off, const int* s_cnt, int G, const BlockD
 #pragma unroll
     for (int c = 0; c < kOrderMaxClasses; ++c) pl = c == lc - 1 ? pos[c] : pl;
     border[pl + (lc == NC ? nfull : 0)] = b0 + nfull;
+  }
+}
+
+// The one-workgroup align; with `border` (BM a multiple of 16, at most 128) it also writes the
+// heaviest-first block order, from the group offsets and slot counts the sort leaves in LDS.
+__global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__ topk_ids, int T,
+                                                     int top_k, int E, int has_shared, int BM,
+                                                     int cap, int32_t* __restrict__ sorted,
+                                                     int32_t* __restrict__ eids,
+                                                     int32_t* __restrict__ ntpp,
+                                                     int32_t* __restrict__ border) {
+  __shared__ AlignSmem sm;
+  __shared__ int s_wtot[kOrderMaxClasses][16];
+  align_block(topk_ids, T, top_k, E, has_shared, BM, cap, sorted, eids, ntpp, sm);
+  if (border) {
+    __syncthreads();  // every wave's scatter is done with its counters
+    const int G = E + (has_shared ? 1 : 0);
+    for (int g = threadIdx.x; g < G; g += 1024) sm.cnt[0][g] = sm.pad[g] - sm.off[g];
+    __syncthreads();
+    block_order(sm.off, sm.cnt[0], G, BlockDiv(BM), s_wtot, border);
   }
 }
 
@@ -395,6 +406,7 @@ hipError_t launch_align(const int32_t* topk_ids, int T, int top_k, int E, int ha
     return hipGetLastError();
   }
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, topk_ids, T, top_k, E,
-                     has_shared, BM, cap, sorted, eids, ntpp);
+                     has_shared, BM, cap, sorted, eids, ntpp,
+                     (BM % 16 == 0 && BM <= 16 * kOrderMaxClasses) ? border : nullptr);
   return hipGetLastError();
 }

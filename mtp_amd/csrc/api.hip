@@ -95,7 +95,7 @@ ExpertsDev make_experts_dev(const moe_expert_set_v1* ex, const moe_expert_set_v1
 int resolve_path(int path, int T, int top_k) {
   if (path == MOE_PATH_DECODE || path == MOE_PATH_PREFILL) return path;
   if (path != MOE_PATH_AUTO) return -1;
-  return (T * top_k >= 1024) ? MOE_PATH_PREFILL : MOE_PATH_DECODE;
+  return ((int64_t)T * top_k >= kAutoPrefillSlots) ? MOE_PATH_PREFILL : MOE_PATH_DECODE;
 }
 
 int block_m_of(int path) { return path == MOE_PATH_PREFILL ? kPrefillBlockM : kDecodeBlockM; }
@@ -176,14 +176,15 @@ int run_experts(const uint16_t* x, int T, int top_k, const moe_expert_set_v1* ex
   uint16_t* h = at<uint16_t>(ws, L.h);
   float* ys = at<float>(ws, L.ys);
   // The large-input align keeps its ranks and chunk counts in the ys section (not in use until
-  // W2) and also orders the blocks for the prefill GEMMs.
+  // W2). Every align form also orders the blocks heaviest first for the prefill GEMMs.
   int32_t* scratch = nullptr;
   if (routing == ROUTE_ALIGN) {
     const int64_t scratch_bytes =
         align_scratch_bytes(T, top_k, ex->num_experts, has_shared, L.bm, L.cap);
     if (scratch_bytes > 0 && (size_t)scratch_bytes <= L.total - L.ys) scratch = at<int32_t>(ws, L.ys);
   }
-  int32_t* border = scratch && path == MOE_PATH_PREFILL ? at<int32_t>(ws, L.border) : nullptr;
+  int32_t* border =
+      routing == ROUTE_ALIGN && path == MOE_PATH_PREFILL ? at<int32_t>(ws, L.border) : nullptr;
   const bool grid = routing == ROUTE_GRID_LOGITS || routing == ROUTE_GRID_IDS;
   if (grid) {
     const SlotGrid sg{1, routing == ROUTE_GRID_LOGITS ? at<float>(ws, L.logits) : nullptr, ids, w};

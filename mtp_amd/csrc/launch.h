@@ -75,8 +75,9 @@ hipError_t launch_shared_gate(const uint16_t* x, int T, int H, const uint16_t* s
 int align_capacity_blocks(int T, int top_k, int E, int has_shared, int BM);
 // Bytes of scratch (outside the output buffers) that lets launch_align spread the large-input
 // scatter over many workgroups, for any number of slots; 0 when these sizes take the one-block
-// kernel. Given such a scratch, launch_align also writes `border` (when non-null): the align
-// blocks sorted by the number of 16-row subtiles holding slots, heaviest first (cap entries).
+// kernel. Every form writes `border` (when non-null and BM is a multiple of 16, at most 128):
+// the align blocks sorted by the number of 16-row subtiles holding slots, heaviest first (one
+// entry per block up to the padded total).
 int64_t align_scratch_bytes(int T, int top_k, int E, int has_shared, int BM, int cap);
 // scratch (nullable): align_scratch_bytes bytes the call may overwrite. Without it, inputs of up to
 // 32 768 slots still take a two-kernel form (ranks and counts in the sorted buffer), larger ones the
@@ -185,6 +186,10 @@ hipError_t launch_router_logits_norm(const uint16_t* res_in, const uint16_t* add
 // Block sizes (slots per block) of the two paths.
 constexpr int kDecodeBlockM = 16;
 constexpr int kPrefillBlockM = 128;
+// AUTO takes the prefill path from this many routed slots (T * top_k) on: below it the decode
+// kernels were faster at hidden 2048, 256 experts, intermediate 512, top-8 with Zipf skew (per
+// layer 112.8 vs 118.1 us at 256 tokens, 126.5 vs 124.8 us at 320 tokens).
+constexpr int kAutoPrefillSlots = 2560;
 
 // HiddenResidualExpertPredictor forward (hr_predictor.hip).
 int64_t hr_predictor_workspace(int N, int W, int F, int E);

@@ -17,6 +17,7 @@ from mtp_amd.weights import MoeExperts
 PATHS = {"auto": _lib.PATH_AUTO, "decode": _lib.PATH_DECODE, "prefill": _lib.PATH_PREFILL}
 DECODE_BLOCK_M = 16
 PREFILL_BLOCK_M = 128
+AUTO_PREFILL_SLOTS = 2560  # routed slots (T * top_k) from which "auto" runs the prefill path
 OUT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
@@ -213,7 +214,7 @@ def align(topk_ids: torch.Tensor, num_experts: int, block_m: int, *, has_shared:
 # ----------------------------------------------------------------------------- GEMMs
 def _block_m(path: int, T: int, top_k: int) -> int:
     if path == _lib.PATH_AUTO:
-        path = _lib.PATH_PREFILL if T * top_k >= 1024 else _lib.PATH_DECODE
+        path = _lib.PATH_PREFILL if T * top_k >= AUTO_PREFILL_SLOTS else _lib.PATH_DECODE
     return PREFILL_BLOCK_M if path == _lib.PATH_PREFILL else DECODE_BLOCK_M
 
 

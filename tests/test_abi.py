@@ -9,7 +9,7 @@ from pathlib import Path
 
 import pytest
 
-from mtp_amd import _lib
+from mtp_amd import _lib, ops
 from oracle import moe_ref
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "moe_w4a16.h"
@@ -145,3 +145,18 @@ def test_noalloc_entry_reports_the_workspace_entrys_error_codes(T, top_k, path, 
     assert rc_ws != _lib.MOE_OK
     assert rc_na == rc_ws
     assert lib.moe_w4a16_last_error() == msg_ws
+
+
+@pytest.mark.parametrize("T,k", [(1, 8), (255, 8), (319, 8), (320, 8), (2048, 8), (2559, 1),
+                                 (2560, 1), (40, 64)])
+def test_auto_path_switches_at_the_measured_slot_count(T, k):
+    """AUTO runs the decode kernels below 2 560 routed slots and the prefill kernels from there
+    on (the two paths' workspaces differ in their block tables, so the query shows which)."""
+    lib = _lib.load()
+    ex = _fake_set()
+    sizes = {p: lib.moe_layer_workspace_bytes_v1(T, k, ctypes.byref(ex), 0, p)
+             for p in (_lib.PATH_AUTO, _lib.PATH_DECODE, _lib.PATH_PREFILL)}
+    assert sizes[_lib.PATH_DECODE] != sizes[_lib.PATH_PREFILL]
+    want = _lib.PATH_PREFILL if T * k >= 2560 else _lib.PATH_DECODE
+    assert sizes[_lib.PATH_AUTO] == sizes[want]
+    assert ops._block_m(_lib.PATH_AUTO, T, k) == (128 if want == _lib.PATH_PREFILL else 16)

@@ -59,9 +59,10 @@ def test_token_sum_w2_with_shared_expert(T):
 
 
 @pytest.mark.parametrize("T,path", [(16, "decode"), (16, "prefill"), (1, "decode"), (32, "decode"),
-                                    (64, "decode")])
+                                    (64, "decode"), (256, "auto"), (320, "auto")])
 def test_config1_full_shape(T, path):
-    """Config 1: hidden 2048, 256 experts, intermediate 512, top-8, 16 tokens."""
+    """Config 1: hidden 2048, 256 experts, intermediate 512, top-8, 16 tokens; and batches on
+    either side of the auto path switch (2 048 slots: decode, 2 560: prefill)."""
     _say(f"config1 T={T} path={path}")
     _check_layer(synth.make_layer(0), T, 8, path)
 
@@ -424,7 +425,7 @@ def test_max_expert_count_with_shared_expert(T, path, top_k):
 
 
 @pytest.mark.parametrize("T,path,top_k", [(1, "decode", 1), (7, "decode", 1), (64, "decode", 2),
-                                          (300, "prefill", 1), (1100, "auto", 1),
+                                          (300, "prefill", 1), (2600, "auto", 1),
                                           (700, "auto", 2)])
 def test_one_and_two_experts_per_token(T, path, top_k):
     """top_k 1 and 2 (the renormalised weight of a single expert is exactly 1): every routing

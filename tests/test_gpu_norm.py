@@ -91,7 +91,7 @@ def test_decode_chain_through_norm():
     (1, False, True, False, "decode"), (2, True, True, False, "decode"),
     (5, False, False, False, "decode"), (16, False, True, False, "decode"),
     (64, True, True, False, "decode"), (7, False, True, True, "decode"),
-    (300, False, True, False, "auto")])
+    (300, False, True, False, "prefill"), (300, True, True, False, "auto")])
 def test_norm_layer_equals_norm_then_layer(T, shared, with_add, in_place, path):
     """moe_norm_layer_v1 gives the bits of moe_rmsnorm_v1 followed by moe_layer_v1: on decode
     batches the router normalises its own tokens (same arithmetic as the norm kernel); in place

@@ -43,7 +43,7 @@ def test_noalloc_layer_matches_workspace_layer_on_consecutive_calls():
     layer = synth.layer_to(synth.make_layer(11, zipf=True, shared=True), "cuda")
     # the second call is smaller and takes another path: the scratch keeps the first call's
     # bytes, which the layer must not depend on
-    for T, path, shared in ((256, "auto", True), (5, "decode", False)):
+    for T, path, shared in ((384, "auto", True), (5, "decode", False)):
         print(f"noalloc T={T} path={path} shared={shared}", flush=True)
         x = synth.make_tokens(T, seed=300 + T).cuda()
         rc, out, ids, w = _noalloc(lib, x, layer, 8, path, shared)
