@@ -11,7 +11,8 @@ expert read comes from HBM.
 value = decode expert-weight HBM GB/s over the whole sweep: sum over batches and layers of
 U_l(T) * 1 634 304 B (distinct routed experts x packed qweight+scales+qzeros per expert) divided
 by the summed median chain time. Also reported: per-batch us/layer and GB/s, prefill-2048
-TFLOP/s (103.08 GFLOP per layer), the W1 decode kernel's roofline (live HIP events), and the CPU
+TFLOP/s (103.08 GFLOP per layer) and the same layers at further batch sizes (256 and 8192 tokens
+by default, on AUTO's path), the W1 decode kernel's roofline (live HIP events), and the CPU
 baseline (the oracle's reference-faithful bf16 path on host cores, bounded sample).
 """
 
@@ -45,6 +46,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=40)
     p.add_argument("--batches", default="1,8,32,64")
     p.add_argument("--prefill-tokens", type=int, default=2048)
+    p.add_argument("--prefill-sizes", default="256,8192",
+                   help="further token counts timed like the prefill batch (empty disables)")
     p.add_argument("--prefill-layers", type=int, default=8,
                    help="resident layers chained in the prefill graph (per-layer time: replay / "
                         "layers)")
@@ -332,10 +335,7 @@ def main() -> int:
     # ------------------------------------------------------------------ prefill-2048
     # A chain of the first `prefill_layers` resident layers in one graph (as the decode chains),
     # per-layer time = replay / layers; layer 0 alone per replay is reported beside it.
-    Tp = args.prefill_tokens
-    prefill = {}
-    if Tp > 0:
-        NLp = max(1, min(args.prefill_layers, len(layers)))
+    def measure_prefill(Tp: int, NLp: int) -> dict:
         xp = synth.make_tokens(Tp, seed=7, device=dev)
         wsps, outps, us = [], [], []
         counts = None
@@ -385,11 +385,19 @@ def main() -> int:
         prefill["GBps"] = prefill["expert_bytes"] / (med * 1e-3) / 1e9
         prefill["hbm_frac"] = prefill["GBps"] / HBM_PEAK_GBPS
         prefill["router_flop"] = 2 * Tp * E * H
+        prefill["path"] = "prefill" if Tp * K >= ops.AUTO_PREFILL_SLOTS else "decode"
         log(f"[bench] prefill T={Tp}: {med * 1e3:.1f} us/layer over {NLp} chained layers "
             f"(layer 0 alone per replay {single * 1e3:.1f} us), {prefill['TFLOPs']:.1f} TFLOP/s "
             f"({100 * prefill['mfma_frac']:.1f}% of bf16 MFMA peak); expert bytes "
             f"{prefill['expert_bytes'] / 1e6:.1f} MB at {prefill['GBps']:.0f} GB/s "
-            f"({100 * prefill['hbm_frac']:.1f}% of 8 TB/s)")
+            f"({100 * prefill['hbm_frac']:.1f}% of 8 TB/s); {prefill['path']} kernels")
+        return prefill
+
+    NLp = max(1, min(args.prefill_layers, len(layers)))
+    prefill = measure_prefill(args.prefill_tokens, NLp) if args.prefill_tokens > 0 else {}
+    # other batch sizes through the same layers (AUTO's path), reported beside the headline
+    prefill_sizes = [measure_prefill(t, NLp) for t in
+                     (int(v) for v in args.prefill_sizes.split(",") if v) if t > 0]
 
     # ------------------------------------------------------- full block with shared expert
     block = {}
@@ -501,7 +509,7 @@ def main() -> int:
     cpu = None
     if args.cpu_baseline_seconds > 0:
         cpu = cpu_baseline(layers, batches, args.cpu_baseline_seconds, per_expert,
-                           Tp if Tp > 0 else 0, block_batches)
+                           max(args.prefill_tokens, 0), block_batches)
 
     result = {
         "metric": METRIC,
@@ -528,6 +536,7 @@ def main() -> int:
         "decode": {str(T): decode[T] for T in batches},
         "decode_buckets": buckets,
         "prefill": prefill,
+        "prefill_sizes": prefill_sizes,
         "block": block,
         "decode_chain": chain,
         "offload": offload,
