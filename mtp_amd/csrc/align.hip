@@ -363,7 +363,7 @@ int align_chunks(int T, int top_k, int E, int has_shared, int BM, int cap, bool 
   const int G = E + (has_shared ? 1 : 0);
   int nchunks = kAlign2LdsCounts / G;
   if (nchunks > kAlign2MaxChunks) nchunks = kAlign2MaxChunks;
-  if (n_slots < 4096 || BM < 64 || BM > 16 * kOrderMaxClasses || nchunks <= 0 || G > kMaxGroups)
+  if (n_slots < 2048 || BM < 64 || BM > 16 * kOrderMaxClasses || nchunks <= 0 || G > kMaxGroups)
     return 0;
   if (!scratch && (n_slots > 1024 * kAlign2MaxSlotsPerThread ||
                    (int64_t)cap * BM < (int64_t)n_slots + (int64_t)nchunks * G))

@@ -109,7 +109,9 @@ def test_router_ties_break_to_lower_id():
                                                   (40, 8, 64, 24, False, False),
                                                   (5, 3, 16, 12, True, False),
                                                   (2048, 8, 256, 96, False, True),
-                                                  # past the two-kernel form's 32 768 slots
+                                                  # the two-kernel form from 2 048 slots, and
+                                                  # past its 32 768 slots
+                                                  (300, 8, 256, 128, True, True),
                                                   (5000, 8, 256, 128, True, True)])
 def test_align_bit_exact(T, k, E, BM, shared, zipf):
     _say(f"align T={T} k={k} E={E} BM={BM} shared={shared} zipf={zipf}")
